@@ -1,0 +1,148 @@
+/* qmhip.h -- C-ABI of the MI355X (gfx950) HIP token loop for quillm.
+ *
+ * Plain C: pointers, sizes and int return codes; no C++ or torch types. Every entry point
+ * names the reference interface it stands in for (file:line in the reference tree).
+ *
+ * Conventions (mirroring the reference's, see its src/model.h:32-36 and src/ops.h:23-34):
+ *   - op-level functions take DEVICE pointers and a stream (NULL = the library's stream) and
+ *     return 0, or -1 with a message in qmh_last_error(). They are asynchronous on the stream.
+ *   - model-level functions take host arguments; forward returns model-owned (pinned host)
+ *     logits, valid until the next call, or NULL on a bad token/pos, like the reference.
+ *   - results are bitwise identical to the reference's scalar ISA path
+ *     (src/kernels_scalar.c) and bitwise reproducible run to run.
+ *   - nothing here allocates on the host heap per token; device memory is allocated at
+ *     model creation only.
+ */
+#ifndef QMHIP_H
+#define QMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* tensor dtypes, same codes as the reference's qm_dtype (src/qm_base.h:11-15) */
+enum { QMH_F32 = 0, QMH_Q8_0 = 2, QMH_Q4_0 = 3 };
+
+/* ------------------------------------------------------------------ runtime */
+
+/* 1 if a gfx950 device is visible. Stands in for qm_cpu_supports(QM_ISA_HIP) next to the
+ * ISA probe of src/cpu.c:39-49. */
+int qmh_available(void);
+/* Select a device and create the library stream. 0 or -1. Stands in for qm_kernels_select
+ * (src/kernels_scalar.c:71-76) for the "hip" ISA. */
+int qmh_init(int device);
+/* Thread-local message for the last -1/NULL return. */
+const char *qmh_last_error(void);
+/* The library's HIP stream (a hipStream_t) -- lets callers order their own work after ours. */
+void *qmh_stream(void);
+
+/* device memory plumbing for callers that hold no HIP runtime of their own */
+void *qmh_dev_alloc(size_t bytes);
+int qmh_dev_free(void *p);
+int qmh_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int qmh_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int qmh_memset(void *dst, int value, size_t bytes);
+int qmh_sync(void);
+
+/* ------------------------------------------------------------------ op level (device pointers) */
+
+/* fp16 <-> fp32, elementwise over n values. qm_fp16_to_fp32 / qm_fp32_to_fp16 (src/fp16.c:6-56) */
+int qmh_fp16_to_fp32(const uint16_t *h, float *f, int64_t n, void *stream);
+int qmh_fp32_to_fp16(const float *f, uint16_t *h, int64_t n, void *stream);
+
+/* rows x n floats -> rows rows of Q8_0 / Q4_0 blocks in the reference byte layout (34 / 18 B
+ * per 32 values, zero padded). qm_quantize_row_q8 / qm_quantize_row_q4 (src/quant.c:55-85). */
+int qmh_quantize_rows_q8(const float *x, void *y, int64_t rows, int64_t n, void *stream);
+int qmh_quantize_rows_q4(const float *x, void *y, int64_t rows, int64_t n, void *stream);
+/* one row of any dtype -> n floats. qm_row_to_f32 (src/quant.c:96-101) */
+int qmh_row_to_f32(int dtype, const void *row, float *y, int64_t n, void *stream);
+
+/* A weight matrix resident on the device, repacked from the reference's row layout
+ * (qm_tensor rows of qm_row_bytes, src/ops.h:8-22) into the tile layout the matvec reads. */
+typedef struct qmh_weight qmh_weight;
+/* host_rows: rows x cols in the .qlm / qm_tensor layout. NULL on error. */
+qmh_weight *qmh_weight_upload(int dtype, int64_t rows, int64_t cols, const void *host_rows);
+void qmh_weight_free(qmh_weight *w);
+
+/* y[rows] = W x. For quantized W, x is quantized to Q8_0 first and, if xq is not NULL, the
+ * quantized blocks are also written there (reference layout). qm_matvec (src/ops.c:57-61)
+ * with the per-row dot_f32 / dot_q8 / dot_q4 of src/kernels_scalar.c:6-34. */
+int qmh_matvec(const qmh_weight *W, const float *x, float *y, void *xq, void *stream);
+
+/* C[M,N] = A[M,K] B[N,K]^T, all row-major contiguous f32. qm_matmul_nt (src/ops.c:81-90) ->
+ * gemm_nt (src/gemm_driver.h:7-28), scalar-ISA rounding order (K panels of 256). */
+int qmh_matmul_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* elementwise ops of src/ops.c:93-133 (in-place where the reference is in place) */
+int qmh_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps, void *stream);
+int qmh_softmax(float *x, int64_t n, void *stream);
+int qmh_rope(float *v, int64_t n_heads, int64_t head_dim, int64_t pos, float theta, void *stream);
+int qmh_swiglu(float *gate, const float *up, int64_t n, void *stream);
+/* *out = first index of the maximum. qm_argmax (src/sampler.c:27-32) */
+int qmh_argmax(const float *x, int32_t n, int32_t *out, void *stream);
+
+/* ------------------------------------------------------------------ model level (host arguments) */
+
+/* qm_config (src/model.h:8-11) */
+typedef struct {
+    int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, max_seq;
+    float rope_theta, norm_eps;
+} qmh_config;
+
+/* A host tensor as the reference's qm_tensor describes it (src/ops.h:9-15): dtype, shape
+ * (ne[0] outermost) and a pointer to rows of qm_row_bytes. */
+typedef struct {
+    int32_t dtype;
+    int32_t ndim;
+    int64_t ne[4];
+    const void *data;
+} qmh_tensor_view;
+
+typedef struct qmh_model qmh_model;
+
+/* Build the device model from host tensors the caller already holds (the reference's
+ * qm_model after qm_model_load, src/model.c:35-117). layers[9*l + k] is layer l's
+ * {attn_norm, wq, wk, wv, wo, ffn_norm, w1, w2, w3}[k] (src/model.h:13-15). Shapes are
+ * validated as src/model.c:20-32,48-77 do. cfg->max_seq sizes the KV cache. NULL on error. */
+qmh_model *qmh_model_create(const qmh_config *cfg, const qmh_tensor_view *tok_embd, const qmh_tensor_view *norm,
+                            const qmh_tensor_view *output, const qmh_tensor_view *layers);
+/* Open a .qlm file (format of src/qlm_file.h:1-9) and create the device model from it.
+ * max_seq <= 0 keeps the file's context, else caps it (src/model.c:53). NULL on error. */
+qmh_model *qmh_model_load(const char *path, int32_t max_seq);
+void qmh_model_free(qmh_model *m);
+const qmh_config *qmh_model_config(const qmh_model *m);
+
+/* One token at position pos; returns model-owned logits[vocab] in pinned host memory, or
+ * NULL for token outside [0, vocab) or pos outside [0, max_seq). qm_model_forward
+ * (src/model.c:158-191). */
+float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos);
+
+/* n tokens at positions pos0..pos0+n-1 in one batched pass. KV cache contents and logits are
+ * bitwise those of n sequential qmh_model_forward calls (the reference's prompt loop,
+ * src/main.c:127-130). logits: NULL, or host memory for n*vocab floats. 0 or -1. */
+int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits);
+
+/* Greedy decode on the device: n_steps forwards starting with token at pos, each next token
+ * the first argmax of the previous logits (reference bench/bench.c:143-149). out[0..n_steps]
+ * receives the argmax after each step (n_steps ids). No host round trip between steps. */
+int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
+
+/* ------------------------------------------------------------------ synthetic models */
+
+/* Write a random-init .qlm (format src/qlm_file.h:1-9, tensor order of the reference's
+ * writer): every 2-D tensor ~ N(0, 0.02) from a counter-based generator keyed by (seed,
+ * tensor, element) and stored as wtype; norm gains 1.0. Results do not depend on n_threads.
+ * 0 or -1. No reference counterpart in C (the reference's generator is its Python tooling). */
+int qmh_gen_qlm(const char *path, const qmh_config *cfg, int wtype, uint64_t seed, int n_threads);
+/* The f32 values (before quantization) of elements [k0, k0+n) of tensor number tensor_index
+ * (its position in the file's tensor table) of a model written by qmh_gen_qlm with `seed`;
+ * lets a checker re-quantize them with another quantizer. */
+void qmh_gen_values(uint64_t seed, int tensor_index, int64_t k0, int64_t n, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,145 @@
+// Device-side numerics shared by the gfx950 kernels.
+//
+// Everything here reproduces the reference's scalar CPU arithmetic bit for bit. The file is
+// compiled with -ffp-contract=off, so a*b+c is two roundings, as in the reference (ISO C
+// mode, no FMA); the only fused multiply-adds are the explicit fma() calls in qmh_expf.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QMH_WG 256  // threads per workgroup for the streaming kernels (4 wave64)
+
+// fp16 bits -> float. v_cvt_f32_f16 is exact for every finite half, subnormals included
+// (fp16 denormals are on by default on gfx9); reference src/fp16.c:6-31.
+__device__ __forceinline__ float qmh_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// float -> fp16 bits, round to nearest even, as reference src/fp16.c:33-56 for the values the
+// quantizer produces (non-negative scales; NaN kept quiet with its top payload bits).
+// Integer-only so the result does not depend on the MODE register.
+__device__ __forceinline__ uint16_t qmh_f2h(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    int e = (int)(a >> 23) - 127;                        // unbiased exponent
+    if (e >= 16) return (uint16_t)(sign | 0x7c00u);       // 2^16 and up (and inf) -> inf
+    if (e < -25) return (uint16_t)sign;                   // below 2^-25 -> signed zero
+    uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+    int sh = e >= -14 ? 13 : 13 + (-14 - e);              // 13 (normal) .. 24 (deep subnormal)
+    uint32_t q = mant >> sh, rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+    // a normal q carries the implicit bit, so adding the biased exponent minus one both
+    // places it and lets a rounding carry roll into the exponent (65520 -> inf)
+    uint32_t r = e >= -14 ? (((uint32_t)(e + 14) << 10) + q) : q;
+    return (uint16_t)(sign | r);
+}
+
+// expf exactly as the host's glibc computes it (glibc >= 2.27 uses the ARM optimized-routines
+// algorithm: x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, a cubic for 2^(r/32), all in
+// double, x86-64 FMA build). Checked equal to glibc expf for all 2^32 inputs on the host.
+// The reference calls expf in softmax and SwiGLU (src/ops.c:107,131).
+__constant__ static const uint64_t qmh_exp2_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__device__ __forceinline__ float qmh_expf(float x) {
+    uint32_t ux = __float_as_uint(x);
+    uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    uint64_t t = qmh_exp2_tab[ki % 32] + (ki << 47);
+    double s = __longlong_as_double((long long)t);
+    double z = __builtin_fma(c0, r, c1);
+    double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// --------------------------------------------------------------------------- reductions
+
+__device__ __forceinline__ float qmh_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ double qmh_wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Workgroup-wide sum of doubles (fixed tree: wave butterflies, then waves in order), result
+// broadcast to all threads. buf: >= 16 doubles of LDS. Deterministic for a given blockDim.
+__device__ __forceinline__ double qmh_block_sum_d(double v, double *buf) {
+    v = qmh_wave_sum_d(v);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) buf[w] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int i = 0; i < nw; i++) s += buf[i];
+    return s;
+}
+
+__device__ __forceinline__ float qmh_block_max(float v, float *buf) {
+    v = qmh_wave_max(v);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) buf[w] = v;
+    __syncthreads();
+    float m = buf[0];
+    for (int i = 1; i < nw; i++) m = fmaxf(m, buf[i]);
+    return m;
+}
+
+// --------------------------------------------------------------------------- quantization
+
+// One Q8_0 code: clamp(rint(v/dd), -127, 127), 0 when dd == 0 (reference src/quant.c:48-53).
+// v/dd is the correctly rounded IEEE division (hipcc default), rintf is v_rndne_f32.
+__device__ __forceinline__ int qmh_q8_code(float v, float dd) {
+    if (dd == 0.0f) return 0;
+    float r = rintf(v / dd);
+    r = r < -127.0f ? -127.0f : r;
+    r = r > 127.0f ? 127.0f : r;
+    return (int)r;
+}
+__device__ __forceinline__ int qmh_q4_code(float v, float dd) {
+    if (dd == 0.0f) return 0;
+    float r = rintf(v / dd);
+    r = r < -8.0f ? -8.0f : r;
+    r = r > 7.0f ? 7.0f : r;
+    return (int)r;
+}
+
+// amax of a block spread over 8 consecutive lanes (4 values each): NaN never wins, like the
+// reference's `a > amax` scan (src/quant.c:38-42).
+__device__ __forceinline__ float qmh_amax8(float m) {
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        float p = __shfl_xor(m, o);
+        m = p > m ? p : m;
+    }
+    return m;
+}

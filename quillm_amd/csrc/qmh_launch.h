@@ -1,0 +1,80 @@
+/* Internal C interface between the C11 host code (quillm_amd/host) and the HIP kernels
+ * (quillm_amd/csrc). Plain C types only; every launcher enqueues on `stream` (a
+ * hipStream_t) and returns a hipError_t as int (0 = success). */
+#ifndef QMH_LAUNCH_H
+#define QMH_LAUNCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* rows per tile of the device weight layout */
+#define QMH_TILE_R 16
+
+/* matvec epilogues */
+enum {
+    QMH_EPI_STORE = 0,  /* out0[row] = y */
+    QMH_EPI_ADD = 1,    /* out0[row] = out0[row] + y  (residual, src/model.c:179,186) */
+    QMH_EPI_QKV = 2,    /* rows [0,seg1): q with RoPE -> out0; [seg1,seg2): k with RoPE -> K cache
+                           row pos (out1); [seg2,rows): v -> transposed V cache column pos (out2) */
+    QMH_EPI_SWIGLU = 3, /* interleaved W1|W3 tiles: out0[row] = silu(y1)*y3 (src/ops.c:128-133) */
+};
+
+typedef struct {
+    /* weight: tiled codes/scales (quantized) or row-major floats (f32) */
+    int dtype;
+    const void *codes;
+    const uint16_t *scales;
+    int nb;      /* blocks per row (quantized) */
+    int cols;    /* elements per row */
+    int tile_r;  /* rows per tile: QMH_TILE_R, or 2*QMH_TILE_R for interleaved W1|W3 */
+    int ntiles;
+    int rows;    /* valid output rows (per half for the interleaved W1|W3) */
+    /* activation: x[cols]; optional RMSNorm gain (norm_w != NULL) applied before quantization */
+    const float *x;
+    const float *norm_w;
+    float eps;
+    uint8_t *xq_out; /* optional: quantized activation in the reference Q8_0 layout */
+    /* epilogue */
+    int epi;
+    float *out0, *out1, *out2;
+    int seg1, seg2;
+    const float *rope; /* [max_seq][head_dim/2][2] (cos, sin) */
+    const int32_t *pos_ptr;
+    int head_dim, max_seq, kvd;
+} qmh_mv_args;
+
+int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes, uint16_t *scales,
+                      int tile_r, int64_t row_off, int interleave_half, void *stream);
+int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
+/* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
+int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
+
+int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, const int32_t *tok_ptr, float *x, void *stream);
+int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, const int32_t *pos_ptr, int n_heads,
+                           int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
+int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
+                       int n_kv_heads, int head_dim, int max_seq, void *stream);
+/* argmax over x[n] -> *out_idx; if tokpos != NULL also tokpos[0] = idx, tokpos[1] += 1 and
+ * record[step] = idx where step = tokpos[2]++ (device greedy loop state) */
+int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record, void *stream);
+/* gate = silu(gate)*up over n (src/ops.c:128-133) */
+int qmh_launch_swiglu(float *gate, const float *up, int64_t n, void *stream);
+
+/* op-level kernels */
+int qmh_launch_h2f(const uint16_t *h, float *f, int64_t n, void *stream);
+int qmh_launch_f2h(const float *f, uint16_t *h, int64_t n, void *stream);
+int qmh_launch_quantize_rows(const float *x, uint8_t *y, int64_t rows, int64_t n, int dtype, void *stream);
+int qmh_launch_row_to_f32(const uint8_t *row, int dtype, float *y, int64_t n, void *stream);
+int qmh_launch_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps, void *stream);
+int qmh_launch_softmax(float *x, int64_t n, void *stream);
+int qmh_launch_rope(float *v, int64_t n_heads, int64_t head_dim, const float *table, int64_t pos, void *stream);
+int qmh_launch_gemm_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,701 @@
+/* HIP host runtime for the quillm token loop: C11 on the HIP runtime C API.
+ *
+ * Owns the device, the library stream, device weights (repacked from the reference's row
+ * layout), and the device model: one hipGraph per decode step, replayed with the token and
+ * position read from device memory, so forward(token, pos) costs one small copy in, one graph
+ * launch and one logits copy out, and the greedy loop never returns to the host. */
+#define _DEFAULT_SOURCE
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/qmhip.h"
+#include "../csrc/qmh_launch.h"
+#include "qlm_io.h"
+
+int qmh_gen_qlm_impl(const char *path, const qmh_config *cfg, int wtype, uint64_t seed, int n_threads, char *err,
+                     size_t errlen);
+
+/* ------------------------------------------------------------------ errors */
+
+static _Thread_local char g_err[512];
+
+static int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+const char *qmh_last_error(void) { return g_err; }
+
+#define HIPCHK(call)                                                                                                  \
+    do {                                                                                                              \
+        hipError_t e_ = (call);                                                                                       \
+        if (e_ != hipSuccess) return fail("%s failed: %s", #call, hipGetErrorString(e_));                            \
+    } while (0)
+#define LCHK(call)                                                                                                    \
+    do {                                                                                                              \
+        int e_ = (call);                                                                                              \
+        if (e_ != 0) return fail("%s failed: %s", #call, hipGetErrorString((hipError_t)e_));                         \
+    } while (0)
+
+/* ------------------------------------------------------------------ runtime */
+
+static int g_ready, g_dev = -1, g_cus = 256;
+static hipStream_t g_stream;
+static float *g_rope_scratch; /* op-level rope: one position's (cos, sin) pairs */
+#define ROPE_SCRATCH_PAIRS 4096
+
+int qmh_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    for (int i = 0; i < n; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) == hipSuccess && strncmp(p.gcnArchName, "gfx950", 6) == 0) return 1;
+    }
+    return 0;
+}
+
+int qmh_init(int device) {
+    if (g_ready && device == g_dev) return 0;
+    if (g_ready) return fail("qmh_init: already initialised on device %d", g_dev);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return fail("no HIP device %d", device);
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail("device %d is %s; this library is built for gfx950 only", device, p.gcnArchName);
+    HIPCHK(hipSetDevice(device));
+    HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    HIPCHK(hipMalloc((void **)&g_rope_scratch, sizeof(float) * 2 * ROPE_SCRATCH_PAIRS));
+    g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    g_dev = device;
+    g_ready = 1;
+    return 0;
+}
+
+static int ensure(void) { return g_ready ? 0 : qmh_init(0); }
+static hipStream_t S(void *stream) { return stream ? (hipStream_t)stream : g_stream; }
+
+void *qmh_stream(void) { return ensure() ? NULL : (void *)g_stream; }
+
+void *qmh_dev_alloc(size_t bytes) {
+    void *p = NULL;
+    if (ensure()) return NULL;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        fail("hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return NULL;
+    }
+    return p;
+}
+int qmh_dev_free(void *p) {
+    if (p) HIPCHK(hipFree(p));
+    return 0;
+}
+int qmh_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    if (ensure()) return -1;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+int qmh_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    if (ensure()) return -1;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+int qmh_memset(void *dst, int value, size_t bytes) {
+    if (ensure()) return -1;
+    HIPCHK(hipMemsetAsync(dst, value, bytes, g_stream));
+    return 0;
+}
+int qmh_sync(void) {
+    if (ensure()) return -1;
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+/* ------------------------------------------------------------------ op level */
+
+int qmh_fp16_to_fp32(const uint16_t *h, float *f, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_h2f(h, f, n, S(stream)));
+    return 0;
+}
+int qmh_fp32_to_fp16(const float *f, uint16_t *h, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_f2h(f, h, n, S(stream)));
+    return 0;
+}
+int qmh_quantize_rows_q8(const float *x, void *y, int64_t rows, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_quantize_rows(x, y, rows, n, QMH_Q8_0, S(stream)));
+    return 0;
+}
+int qmh_quantize_rows_q4(const float *x, void *y, int64_t rows, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_quantize_rows(x, y, rows, n, QMH_Q4_0, S(stream)));
+    return 0;
+}
+int qmh_row_to_f32(int dtype, const void *row, float *y, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    if (!(dtype == QMH_F32 || dtype == QMH_Q8_0 || dtype == QMH_Q4_0)) return fail("bad dtype %d", dtype);
+    LCHK(qmh_launch_row_to_f32(row, dtype, y, n, S(stream)));
+    return 0;
+}
+int qmh_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_rmsnorm(out, x, w, n, eps, S(stream)));
+    return 0;
+}
+int qmh_softmax(float *x, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_softmax(x, n, S(stream)));
+    return 0;
+}
+int qmh_swiglu(float *gate, const float *up, int64_t n, void *stream) {
+    if (ensure()) return -1;
+    LCHK(qmh_launch_swiglu(gate, up, n, S(stream)));
+    return 0;
+}
+int qmh_argmax(const float *x, int32_t n, int32_t *out, void *stream) {
+    if (ensure()) return -1;
+    if (n < 1) return fail("argmax of an empty vector");
+    LCHK(qmh_launch_argmax(x, n, out, NULL, NULL, S(stream)));
+    return 0;
+}
+
+/* (cos, sin) of position pos for pair i, in the reference's double formula (src/ops.c:116-118),
+ * rounded to fp32 on the host so the device rotates with bit-identical factors */
+static void rope_pairs(float *out, int64_t head_dim, int64_t pos, float theta) {
+    for (int64_t i = 0; i < head_dim / 2; i++) {
+        double freq = pow((double)theta, -2.0 * (double)i / (double)head_dim);
+        double ang = (double)pos * freq;
+        out[2 * i] = (float)cos(ang);
+        out[2 * i + 1] = (float)sin(ang);
+    }
+}
+
+int qmh_rope(float *v, int64_t n_heads, int64_t head_dim, int64_t pos, float theta, void *stream) {
+    if (ensure()) return -1;
+    if (head_dim / 2 > ROPE_SCRATCH_PAIRS || head_dim < 0 || n_heads < 0) return fail("rope: head_dim too large");
+    float cs[2 * ROPE_SCRATCH_PAIRS];
+    rope_pairs(cs, head_dim, pos, theta);
+    HIPCHK(hipStreamSynchronize(S(stream))); /* scratch is shared by every call */
+    HIPCHK(hipMemcpy(g_rope_scratch, cs, sizeof(float) * (size_t)head_dim, hipMemcpyHostToDevice));
+    LCHK(qmh_launch_rope(v, n_heads, head_dim, g_rope_scratch, 0, S(stream)));
+    HIPCHK(hipStreamSynchronize(S(stream)));
+    return 0;
+}
+
+int qmh_matmul_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K, void *stream) {
+    if (ensure()) return -1;
+    if (M < 0 || N < 0 || K < 0) return fail("matmul_nt: negative size");
+    LCHK(qmh_launch_gemm_nt(A, B, C, M, N, K, S(stream)));
+    return 0;
+}
+
+/* ------------------------------------------------------------------ device weights */
+
+struct qmh_weight {
+    int dtype, tile_r, nb, ntiles;
+    int64_t rows, cols; /* rows: output rows (per half for an interleaved pair) */
+    void *codes;        /* tiled codes, or row-major f32 */
+    uint16_t *scales;
+};
+
+static void weight_release(struct qmh_weight *w) {
+    if (w->codes) hipFree(w->codes);
+    if (w->scales) hipFree(w->scales);
+    memset(w, 0, sizeof *w);
+}
+
+/* Build a device weight from nsrc host matrices with the same dtype and cols:
+ * interleave = 0: rows appended in order (e.g. [wq; wk; wv]);
+ * interleave = 1: two matrices of equal rows, tile t holding 16 rows of each (w1 | w3). */
+static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *const *src, const int64_t *src_rows,
+                        int64_t cols, int interleave) {
+    memset(w, 0, sizeof *w);
+    w->dtype = dtype;
+    w->cols = cols;
+    w->nb = (int)((cols + 31) / 32);
+    int64_t total = 0;
+    for (int i = 0; i < nsrc; i++) total += src_rows[i];
+    if (dtype == QMH_F32) {
+        w->rows = total;
+        size_t rb = (size_t)cols * 4;
+        HIPCHK(hipMalloc(&w->codes, rb * (size_t)total));
+        size_t off = 0;
+        for (int i = 0; i < nsrc; i++) {
+            HIPCHK(hipMemcpy((uint8_t *)w->codes + off, src[i], rb * (size_t)src_rows[i], hipMemcpyHostToDevice));
+            off += rb * (size_t)src_rows[i];
+        }
+        return 0;
+    }
+    if (dtype != QMH_Q8_0 && dtype != QMH_Q4_0) return fail("unsupported dtype %d", dtype);
+    const int cb = dtype == QMH_Q4_0 ? 16 : 32;
+    const size_t rb = qlm_row_bytes(dtype, cols);
+    if (interleave) {
+        if (nsrc != 2 || src_rows[0] != src_rows[1]) return fail("interleaved weight needs two equal matrices");
+        w->tile_r = 2 * QMH_TILE_R;
+        w->rows = src_rows[0];
+        w->ntiles = (int)((src_rows[0] + QMH_TILE_R - 1) / QMH_TILE_R);
+    } else {
+        w->tile_r = QMH_TILE_R;
+        w->rows = total;
+        w->ntiles = (int)((total + QMH_TILE_R - 1) / QMH_TILE_R);
+    }
+    const size_t slots = (size_t)w->ntiles * (size_t)w->nb * (size_t)w->tile_r;
+    HIPCHK(hipMalloc(&w->codes, slots * (size_t)cb));
+    HIPCHK(hipMalloc((void **)&w->scales, slots * 2));
+    HIPCHK(hipMemsetAsync(w->codes, 0, slots * (size_t)cb, g_stream));
+    HIPCHK(hipMemsetAsync(w->scales, 0, slots * 2, g_stream));
+    size_t maxb = 0;
+    for (int i = 0; i < nsrc; i++) maxb = rb * (size_t)src_rows[i] > maxb ? rb * (size_t)src_rows[i] : maxb;
+    void *stage = NULL;
+    HIPCHK(hipMalloc(&stage, maxb ? maxb : 1));
+    int64_t row_off = 0;
+    int rc = 0;
+    for (int i = 0; i < nsrc && rc == 0; i++) {
+        hipError_t e = hipMemcpyAsync(stage, src[i], rb * (size_t)src_rows[i], hipMemcpyHostToDevice, g_stream);
+        if (e == hipSuccess)
+            e = (hipError_t)qmh_launch_repack(stage, src_rows[i], w->nb, dtype, w->codes, w->scales, w->tile_r,
+                                              row_off, interleave ? i : -1, g_stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+        if (e != hipSuccess) rc = fail("weight upload: %s", hipGetErrorString(e));
+        row_off += src_rows[i];
+    }
+    hipFree(stage);
+    return rc;
+}
+
+qmh_weight *qmh_weight_upload(int dtype, int64_t rows, int64_t cols, const void *host_rows) {
+    if (ensure()) return NULL;
+    if (rows <= 0 || cols <= 0 || !host_rows) {
+        fail("weight_upload: empty matrix");
+        return NULL;
+    }
+    qmh_weight *w = calloc(1, sizeof *w);
+    if (!w) return NULL;
+    const void *src[1] = {host_rows};
+    int64_t r[1] = {rows};
+    if (weight_build(w, dtype, 1, src, r, cols, 0)) {
+        weight_release(w);
+        free(w);
+        return NULL;
+    }
+    return w;
+}
+
+void qmh_weight_free(qmh_weight *w) {
+    if (!w) return;
+    weight_release(w);
+    free(w);
+}
+
+static void mv_args_for(const struct qmh_weight *w, qmh_mv_args *a) {
+    memset(a, 0, sizeof *a);
+    a->dtype = w->dtype;
+    a->codes = w->codes;
+    a->scales = w->scales;
+    a->nb = w->nb;
+    a->cols = (int)w->cols;
+    a->tile_r = w->tile_r;
+    a->ntiles = w->ntiles;
+    a->rows = (int)w->rows;
+}
+
+static int mv_grid_cap(void) { return 2 * g_cus; }
+
+static int mv_launch(const qmh_mv_args *a, hipStream_t s) {
+    return a->dtype == QMH_F32 ? qmh_launch_matvec_f32(a, s) : qmh_launch_matvec(a, mv_grid_cap(), s);
+}
+
+int qmh_matvec(const qmh_weight *W, const float *x, float *y, void *xq, void *stream) {
+    if (ensure()) return -1;
+    if (!W) return fail("matvec: NULL weight");
+    qmh_mv_args a;
+    mv_args_for(W, &a);
+    a.x = x;
+    a.epi = QMH_EPI_STORE;
+    a.out0 = y;
+    a.xq_out = W->dtype == QMH_F32 ? NULL : (uint8_t *)xq;
+    LCHK(mv_launch(&a, S(stream)));
+    return 0;
+}
+
+/* ------------------------------------------------------------------ model */
+
+typedef struct {
+    struct qmh_weight qkv, wo, w13, w2;
+} dev_layer;
+
+struct qmh_model {
+    qmh_config cfg;
+    int hd, kvd, group;
+    int emb_dtype;
+    void *d_embd;
+    float *d_norms; /* [2L+1][D]: attn_norm l, ffn_norm l, ..., final norm */
+    dev_layer *layers;
+    struct qmh_weight output;
+    float *d_rope;  /* [max_seq][hd/2][2] */
+    float *d_x, *d_xb, *d_q, *d_hb, *d_att, *d_logits, *d_k, *d_vt;
+    int32_t *d_tokpos; /* token, pos, step, - */
+    int32_t *d_record; /* greedy ids [max_seq] */
+    int32_t *h_tokpos; /* pinned [max_seq][4] */
+    float *h_logits;   /* pinned [vocab] */
+    hipGraph_t graph_fwd, graph_greedy;
+    hipGraphExec_t exec_fwd, exec_greedy;
+};
+
+static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
+    const qmh_config *c = &m->cfg;
+    const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq;
+    const int32_t *pos_ptr = m->d_tokpos + 1;
+    LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, D, m->d_tokpos, m->d_x, s));
+    for (int l = 0; l < c->n_layers; l++) {
+        dev_layer *L = &m->layers[l];
+        float *kl = m->d_k + (size_t)l * S_ * m->kvd, *vl = m->d_vt + (size_t)l * S_ * m->kvd;
+        qmh_mv_args a;
+        mv_args_for(&L->qkv, &a);
+        a.x = m->d_x;
+        a.norm_w = m->d_norms + (size_t)(2 * l) * D;
+        a.eps = c->norm_eps;
+        a.epi = QMH_EPI_QKV;
+        a.out0 = m->d_q;
+        a.out1 = kl;
+        a.out2 = vl;
+        a.seg1 = D;
+        a.seg2 = D + m->kvd;
+        a.rope = m->d_rope;
+        a.pos_ptr = pos_ptr;
+        a.head_dim = m->hd;
+        a.max_seq = S_;
+        a.kvd = m->kvd;
+        LCHK(mv_launch(&a, s));
+        LCHK(qmh_launch_attn_scores(m->d_q, kl, m->d_att, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_,
+                                    1.0f / sqrtf((float)m->hd), s));
+        LCHK(qmh_launch_attn_pv(m->d_att, vl, m->d_xb, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_, s));
+        mv_args_for(&L->wo, &a);
+        a.x = m->d_xb;
+        a.epi = QMH_EPI_ADD;
+        a.out0 = m->d_x;
+        LCHK(mv_launch(&a, s));
+        mv_args_for(&L->w13, &a);
+        a.x = m->d_x;
+        a.norm_w = m->d_norms + (size_t)(2 * l + 1) * D;
+        a.eps = c->norm_eps;
+        a.out0 = m->d_hb;
+        if (L->w13.dtype == QMH_F32) {
+            a.epi = QMH_EPI_STORE;
+            LCHK(mv_launch(&a, s));
+            LCHK(qmh_launch_swiglu(m->d_hb, m->d_hb + H, H, s));
+        } else {
+            a.epi = QMH_EPI_SWIGLU;
+            LCHK(mv_launch(&a, s));
+        }
+        mv_args_for(&L->w2, &a);
+        a.x = m->d_hb;
+        a.epi = QMH_EPI_ADD;
+        a.out0 = m->d_x;
+        LCHK(mv_launch(&a, s));
+    }
+    qmh_mv_args a;
+    mv_args_for(&m->output, &a);
+    a.x = m->d_x;
+    a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
+    a.eps = c->norm_eps;
+    a.epi = QMH_EPI_STORE;
+    a.out0 = m->d_logits;
+    LCHK(mv_launch(&a, s));
+    if (with_argmax) LCHK(qmh_launch_argmax(m->d_logits, c->vocab_size, NULL, m->d_tokpos, m->d_record, s));
+    return 0;
+}
+
+static int capture(qmh_model *m, int with_argmax, hipGraph_t *g, hipGraphExec_t *ex) {
+    HIPCHK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, g_stream, with_argmax);
+    hipGraph_t graph = NULL;
+    hipError_t e = hipStreamEndCapture(g_stream, &graph);
+    if (rc) {
+        if (graph) hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess) return fail("graph capture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(ex, graph, NULL, NULL, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(graph);
+        return fail("graph instantiate: %s", hipGetErrorString(e));
+    }
+    *g = graph;
+    return 0;
+}
+
+void qmh_model_free(qmh_model *m) {
+    if (!m) return;
+    if (g_ready) hipStreamSynchronize(g_stream);
+    if (m->exec_fwd) hipGraphExecDestroy(m->exec_fwd);
+    if (m->exec_greedy) hipGraphExecDestroy(m->exec_greedy);
+    if (m->graph_fwd) hipGraphDestroy(m->graph_fwd);
+    if (m->graph_greedy) hipGraphDestroy(m->graph_greedy);
+    if (m->layers) {
+        for (int l = 0; l < m->cfg.n_layers; l++) {
+            weight_release(&m->layers[l].qkv);
+            weight_release(&m->layers[l].wo);
+            weight_release(&m->layers[l].w13);
+            weight_release(&m->layers[l].w2);
+        }
+        free(m->layers);
+    }
+    weight_release(&m->output);
+    void *dev[] = {m->d_embd, m->d_norms, m->d_rope, m->d_x,      m->d_xb,     m->d_q, m->d_hb,
+                   m->d_att,  m->d_logits, m->d_k,   m->d_vt, m->d_tokpos, m->d_record};
+    for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
+        if (dev[i]) hipFree(dev[i]);
+    if (m->h_tokpos) hipHostFree(m->h_tokpos);
+    if (m->h_logits) hipHostFree(m->h_logits);
+    free(m);
+}
+
+static int check_view(const qmh_tensor_view *t, const char *name, int64_t d0, int64_t d1) {
+    int ok = t && t->data &&
+             ((d1 == 0 && t->ndim == 1 && t->ne[0] == d0 && t->dtype == QMH_F32) ||
+              (d1 != 0 && t->ndim == 2 && t->ne[0] == d0 && t->ne[1] == d1 &&
+               (t->dtype == QMH_F32 || t->dtype == QMH_Q8_0 || t->dtype == QMH_Q4_0)));
+    return ok ? 0 : fail("missing or mis-shaped tensor '%s'", name);
+}
+
+static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_tensor_view *norm,
+                       const qmh_tensor_view *output, const qmh_tensor_view *layers) {
+    const qmh_config *c = &m->cfg;
+    if (c->dim <= 0 || c->hidden_dim <= 0 || c->n_layers <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 ||
+        c->vocab_size <= 0 || c->max_seq <= 0)
+        return fail("invalid config");
+    /* reference src/model.c:48-52 */
+    if (c->dim % c->n_heads || c->n_heads % c->n_kv_heads || (c->dim / c->n_heads) % 2 || c->n_layers > 1024)
+        return fail("inconsistent head configuration");
+    const int64_t D = c->dim, H = c->hidden_dim, V = c->vocab_size, S_ = c->max_seq;
+    m->hd = c->dim / c->n_heads;
+    m->kvd = m->hd * c->n_kv_heads;
+    m->group = c->n_heads / c->n_kv_heads;
+    const int64_t KV = m->kvd;
+    if (check_view(tok_embd, "tok_embd", V, D) || check_view(norm, "norm", D, 0) || check_view(output, "output", V, D))
+        return -1;
+    static const char *sfx[9] = {"attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w1", "w2", "w3"};
+    const int64_t shp[9][2] = {{D, 0}, {D, D}, {KV, D}, {KV, D}, {D, D}, {D, 0}, {H, D}, {D, H}, {H, D}};
+    for (int l = 0; l < c->n_layers; l++)
+        for (int k = 0; k < 9; k++) {
+            char nm[64];
+            snprintf(nm, sizeof nm, "layers.%d.%s", l, sfx[k]);
+            if (check_view(&layers[9 * l + k], nm, shp[k][0], shp[k][1])) return -1;
+        }
+    for (int l = 0; l < c->n_layers; l++) {
+        const qmh_tensor_view *t = &layers[9 * l];
+        if (t[1].dtype != t[2].dtype || t[1].dtype != t[3].dtype)
+            return fail("layer %d: wq/wk/wv must share one dtype", l);
+        if (t[6].dtype != t[8].dtype) return fail("layer %d: w1/w3 must share one dtype", l);
+    }
+    /* LDS budget of the kernels (64 KiB per workgroup) */
+    const int64_t nbD = (D + 31) / 32, nbH = (H + 31) / 32;
+    if (nbD * (40 + 4 * 2 * QMH_TILE_R) > 65536 || nbH * (40 + 4 * QMH_TILE_R) > 65536 || H > 16384 || D > 16384)
+        return fail("model dims exceed the kernels' LDS budget");
+    if (((int64_t)64 * (m->hd + 1) + (int64_t)m->group * m->hd) * 4 > 65536 || m->group > 15)
+        return fail("head_dim/group too large for the attention kernels");
+
+    HIPCHK(hipMalloc(&m->d_embd, (size_t)V * qlm_row_bytes(tok_embd->dtype, D)));
+    HIPCHK(hipMemcpy(m->d_embd, tok_embd->data, (size_t)V * qlm_row_bytes(tok_embd->dtype, D), hipMemcpyHostToDevice));
+    m->emb_dtype = tok_embd->dtype;
+    HIPCHK(hipMalloc((void **)&m->d_norms, sizeof(float) * (size_t)(2 * c->n_layers + 1) * D));
+    m->layers = calloc((size_t)c->n_layers, sizeof(dev_layer));
+    if (!m->layers) return fail("out of memory");
+    for (int l = 0; l < c->n_layers; l++) {
+        const qmh_tensor_view *t = &layers[9 * l];
+        HIPCHK(hipMemcpy(m->d_norms + (size_t)(2 * l) * D, t[0].data, sizeof(float) * D, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(m->d_norms + (size_t)(2 * l + 1) * D, t[5].data, sizeof(float) * D, hipMemcpyHostToDevice));
+        dev_layer *L = &m->layers[l];
+        const void *qkv[3] = {t[1].data, t[2].data, t[3].data};
+        const int64_t qkv_rows[3] = {D, KV, KV};
+        if (weight_build(&L->qkv, t[1].dtype, 3, qkv, qkv_rows, D, 0)) return -1;
+        const void *wo[1] = {t[4].data};
+        const int64_t wo_rows[1] = {D};
+        if (weight_build(&L->wo, t[4].dtype, 1, wo, wo_rows, D, 0)) return -1;
+        const void *w13[2] = {t[6].data, t[8].data};
+        const int64_t w13_rows[2] = {H, H};
+        if (weight_build(&L->w13, t[6].dtype, 2, w13, w13_rows, D, t[6].dtype != QMH_F32)) return -1;
+        const void *w2[1] = {t[7].data};
+        const int64_t w2_rows[1] = {D};
+        if (weight_build(&L->w2, t[7].dtype, 1, w2, w2_rows, H, 0)) return -1;
+    }
+    HIPCHK(hipMemcpy(m->d_norms + (size_t)(2 * c->n_layers) * D, norm->data, sizeof(float) * D, hipMemcpyHostToDevice));
+    const void *out[1] = {output->data};
+    const int64_t out_rows[1] = {V};
+    if (weight_build(&m->output, output->dtype, 1, out, out_rows, D, 0)) return -1;
+
+    /* RoPE table for every position, reference formula (src/ops.c:114-126) */
+    const size_t pairs = (size_t)S_ * (size_t)(m->hd / 2);
+    float *tab = malloc(sizeof(float) * 2 * (pairs ? pairs : 1));
+    if (!tab) return fail("out of memory");
+    for (int64_t p = 0; p < S_; p++) rope_pairs(tab + (size_t)p * m->hd, m->hd, p, c->rope_theta);
+    hipError_t e = hipMalloc((void **)&m->d_rope, sizeof(float) * 2 * (pairs ? pairs : 1));
+    if (e == hipSuccess) e = hipMemcpy(m->d_rope, tab, sizeof(float) * 2 * pairs, hipMemcpyHostToDevice);
+    free(tab);
+    if (e != hipSuccess) return fail("rope table: %s", hipGetErrorString(e));
+
+    /* activations and caches (zeroed like the reference's arena, src/arena.c:6-15) */
+    const size_t kv_bytes = sizeof(float) * (size_t)c->n_layers * (size_t)S_ * (size_t)KV;
+    HIPCHK(hipMalloc((void **)&m->d_x, sizeof(float) * D));
+    HIPCHK(hipMalloc((void **)&m->d_xb, sizeof(float) * D));
+    HIPCHK(hipMalloc((void **)&m->d_q, sizeof(float) * D));
+    HIPCHK(hipMalloc((void **)&m->d_hb, sizeof(float) * 2 * H));
+    HIPCHK(hipMalloc((void **)&m->d_att, sizeof(float) * (size_t)c->n_heads * S_));
+    HIPCHK(hipMalloc((void **)&m->d_logits, sizeof(float) * V));
+    HIPCHK(hipMalloc((void **)&m->d_k, kv_bytes));
+    HIPCHK(hipMalloc((void **)&m->d_vt, kv_bytes));
+    HIPCHK(hipMalloc((void **)&m->d_tokpos, sizeof(int32_t) * 4));
+    HIPCHK(hipMalloc((void **)&m->d_record, sizeof(int32_t) * (size_t)S_));
+    HIPCHK(hipMemsetAsync(m->d_k, 0, kv_bytes, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_vt, 0, kv_bytes, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
+    HIPCHK(hipHostMalloc((void **)&m->h_tokpos, sizeof(int32_t) * 4 * (size_t)S_, hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void **)&m->h_logits, sizeof(float) * V, hipHostMallocDefault));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    if (capture(m, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
+    if (capture(m, 1, &m->graph_greedy, &m->exec_greedy)) return -1;
+    return 0;
+}
+
+qmh_model *qmh_model_create(const qmh_config *cfg, const qmh_tensor_view *tok_embd, const qmh_tensor_view *norm,
+                            const qmh_tensor_view *output, const qmh_tensor_view *layers) {
+    if (ensure()) return NULL;
+    if (!cfg || !tok_embd || !norm || !output || !layers) {
+        fail("model_create: NULL argument");
+        return NULL;
+    }
+    qmh_model *m = calloc(1, sizeof *m);
+    if (!m) {
+        fail("out of memory");
+        return NULL;
+    }
+    m->cfg = *cfg;
+    if (model_build(m, tok_embd, norm, output, layers)) {
+        char keep[sizeof g_err];
+        memcpy(keep, g_err, sizeof keep);
+        qmh_model_free(m);
+        memcpy(g_err, keep, sizeof keep);
+        return NULL;
+    }
+    return m;
+}
+
+qmh_model *qmh_model_load(const char *path, int32_t max_seq) {
+    if (ensure()) return NULL;
+    qlm_map f;
+    char err[256];
+    if (qlm_map_open(&f, path, err, sizeof err)) {
+        fail("%s", err);
+        return NULL;
+    }
+    static const char *keys[7] = {"llama.dim",        "llama.hidden_dim", "llama.n_layers", "llama.n_heads",
+                                  "llama.n_kv_heads", "llama.vocab_size", "llama.max_seq"};
+    for (int k = 0; k < 7; k++)
+        if (!f.have[k]) { /* reference src/model.c:9-16 */
+            fail("missing/invalid metadata '%s'", keys[k]);
+            qlm_map_close(&f);
+            return NULL;
+        }
+    qmh_config cfg = f.cfg;
+    if (max_seq > 0 && max_seq < cfg.max_seq) cfg.max_seq = max_seq;
+    const qlm_tensor *te = qlm_map_find(&f, "tok_embd"), *tn = qlm_map_find(&f, "norm"),
+                     *to = qlm_map_find(&f, "output");
+    qmh_tensor_view *lv = calloc((size_t)(cfg.n_layers > 0 ? cfg.n_layers : 1) * 9, sizeof(qmh_tensor_view));
+    qmh_model *m = NULL;
+    if (!te || !tn || !to || !lv) {
+        fail("missing or mis-shaped tensor '%s'", !te ? "tok_embd" : !tn ? "norm" : "output");
+        goto done;
+    }
+    static const char *sfx[9] = {"attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w1", "w2", "w3"};
+    for (int l = 0; l < cfg.n_layers && l <= 1024; l++)
+        for (int k = 0; k < 9; k++) {
+            char nm[64];
+            snprintf(nm, sizeof nm, "layers.%d.%s", l, sfx[k]);
+            const qlm_tensor *t = qlm_map_find(&f, nm);
+            if (!t) {
+                fail("missing or mis-shaped tensor '%s'", nm);
+                goto done;
+            }
+            lv[9 * l + k] = t->view;
+        }
+    m = qmh_model_create(&cfg, &te->view, &tn->view, &to->view, lv);
+done:
+    free(lv);
+    qlm_map_close(&f);
+    return m;
+}
+
+const qmh_config *qmh_model_config(const qmh_model *m) { return m ? &m->cfg : NULL; }
+
+float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
+    if (!m || token < 0 || token >= m->cfg.vocab_size || pos < 0 || pos >= m->cfg.max_seq) return NULL;
+    m->h_tokpos[0] = token;
+    m->h_tokpos[1] = pos;
+    hipError_t e = hipMemcpyAsync(m->d_tokpos, m->h_tokpos, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipGraphLaunch(m->exec_fwd, g_stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->h_logits, m->d_logits, sizeof(float) * (size_t)m->cfg.vocab_size, hipMemcpyDeviceToHost,
+                           g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        fail("forward: %s", hipGetErrorString(e));
+        return NULL;
+    }
+    return m->h_logits;
+}
+
+int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits) {
+    if (!m || !tokens || n < 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.max_seq) return fail("prefill: bad range");
+    for (int32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) return fail("prefill: token %d out of range", tokens[i]);
+    const size_t V = (size_t)m->cfg.vocab_size;
+    for (int32_t i = 0; i < n; i++) {
+        int32_t *slot = m->h_tokpos + 4 * (size_t)i;
+        slot[0] = tokens[i];
+        slot[1] = pos0 + i;
+        HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream));
+        HIPCHK(hipGraphLaunch(m->exec_fwd, g_stream));
+        if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * V, m->d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, g_stream));
+    }
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out) {
+    if (!m || n_steps < 0 || token < 0 || token >= m->cfg.vocab_size || pos < 0 ||
+        (int64_t)pos + n_steps > m->cfg.max_seq)
+        return fail("greedy: bad token/range");
+    int32_t *slot = m->h_tokpos;
+    slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
+    HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream));
+    for (int32_t k = 0; k < n_steps; k++) HIPCHK(hipGraphLaunch(m->exec_greedy, g_stream));
+    if (n_steps > 0 && out)
+        HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+/* ------------------------------------------------------------------ generator */
+
+int qmh_gen_qlm(const char *path, const qmh_config *cfg, int wtype, uint64_t seed, int n_threads) {
+    char err[256];
+    if (!path || !cfg) return fail("gen: NULL argument");
+    if (qmh_gen_qlm_impl(path, cfg, wtype, seed, n_threads, err, sizeof err)) return fail("%s", err);
+    return 0;
+}

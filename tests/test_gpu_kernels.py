@@ -1,0 +1,152 @@
+"""Op-level parity of the gfx950 kernels with the CPU oracle, through the C ABI.
+
+The bar is bit-exact equality with the reference's scalar path for every op (integer, byte
+and float results alike). NaN payloads of fp16 decoding are the one documented exception:
+the hardware conversion quiets signalling NaNs, so NaNs are compared by class."""
+import numpy as np
+import pytest
+
+from _bind import F32, Q4_0, Q8_0, nblocks, row_bytes
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(7)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def dev(qmh, a):
+    return qmh.DeviceBuffer.from_array(a)
+
+
+def test_fp16_decode_all_halves(gpu, oracle):
+    h = np.arange(65536, dtype=np.uint16)
+    dh, df = dev(gpu, h), gpu.DeviceBuffer(65536 * 4)
+    gpu._check(gpu.load_library().qmh_fp16_to_fp32(dh.ptr, df.ptr, 65536, None), "h2f")
+    got, want = df.to_array(np.float32), oracle.h2f(h)
+    isn = np.isnan(want)
+    assert np.array_equal(np.isnan(got), isn)
+    assert np.array_equal(bits(got[~isn]), bits(want[~isn]))
+
+
+def test_fp16_encode_sweep(gpu, oracle):
+    u = np.arange(0, 1 << 32, 4099, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([u.view(np.float32), ((rng.random(1 << 20) - 0.5) *
+                                             np.exp2(rng.integers(-30, 18, 1 << 20))).astype(np.float32)])
+    dx, dh = dev(gpu, x), gpu.DeviceBuffer(x.size * 2)
+    gpu._check(gpu.load_library().qmh_fp32_to_fp16(dx.ptr, dh.ptr, x.size, None), "f2h")
+    assert np.array_equal(dh.to_array(np.uint16), oracle.f2h(x))
+
+
+@pytest.mark.parametrize("dtype", [Q8_0, Q4_0])
+def test_quantize_rows_bytes(gpu, oracle, dtype):
+    fn = gpu.load_library().qmh_quantize_rows_q8 if dtype == Q8_0 else gpu.load_library().qmh_quantize_rows_q4
+    for it in range(60):
+        rows, n = int(rng.integers(1, 9)), int(rng.integers(1, 701))
+        x = (rng.standard_normal((rows, n)) * np.exp2(rng.integers(-12, 13))).astype(np.float32)
+        x[0, rng.integers(0, n)] *= 50.0
+        if it % 5 == 0:
+            x[-1, : min(n, 64)] = 0.0
+        dx, dy = dev(gpu, x), gpu.DeviceBuffer(rows * row_bytes(dtype, n))
+        gpu._check(fn(dx.ptr, dy.ptr, rows, n, None), "quantize")
+        assert np.array_equal(dy.to_array(np.uint8).reshape(rows, -1), oracle.quantize(dtype, x)), (rows, n)
+
+
+@pytest.mark.parametrize("dtype", [F32, Q8_0, Q4_0])
+def test_row_to_f32(gpu, oracle, dtype):
+    n = 1000
+    x = rng.standard_normal(n).astype(np.float32)
+    row = x if dtype == F32 else oracle.quantize(dtype, x)[0]
+    dr, dy = dev(gpu, row), gpu.DeviceBuffer(n * 4)
+    gpu._check(gpu.load_library().qmh_row_to_f32(dtype, dr.ptr, dy.ptr, n, None), "row_to_f32")
+    assert np.array_equal(bits(dy.to_array(np.float32)), bits(oracle.row_to_f32(dtype, row, n)))
+
+
+def _matvec_case(gpu, oracle, dtype, rows, cols, scale=1.0):
+    W = (rng.standard_normal((rows, cols)) * scale).astype(np.float32)
+    Wq = W if dtype == F32 else oracle.quantize(dtype, W)
+    x = rng.standard_normal(cols).astype(np.float32)
+    want, want_xq = oracle.matvec(dtype, Wq, rows, cols, x)
+    L = gpu.load_library()
+    h = L.qmh_weight_upload(dtype, rows, cols, np.ascontiguousarray(Wq).ctypes.data)
+    assert h, gpu.last_error()
+    try:
+        dx, dy, dq = dev(gpu, x), gpu.DeviceBuffer(rows * 4), gpu.DeviceBuffer(nblocks(cols) * 34)
+        gpu._check(L.qmh_matvec(h, dx.ptr, dy.ptr, dq.ptr, None), "matvec")
+        got = dy.to_array(np.float32)
+        assert np.array_equal(bits(got), bits(want)), (dtype, rows, cols)
+        if dtype != F32:
+            assert np.array_equal(dq.to_array(np.uint8), want_xq)
+    finally:
+        L.qmh_weight_free(h)
+
+
+@pytest.mark.parametrize("dtype", [F32, Q8_0, Q4_0])
+def test_matvec_random_shapes(gpu, oracle, dtype):
+    for it in range(25):
+        _matvec_case(gpu, oracle, dtype, int(rng.integers(1, 300)), int(rng.integers(1, 400)))
+
+
+@pytest.mark.parametrize("dtype", [Q8_0, Q4_0])
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 288), (288, 768)])
+def test_matvec_model_shapes(gpu, oracle, dtype, rows, cols):
+    _matvec_case(gpu, oracle, dtype, rows, cols, scale=0.02)
+
+
+def test_gemm_nt(gpu, oracle):
+    L = gpu.load_library()
+    shapes = [(4, 4, 8), (512, 512, 512), (17, 130, 600), (1, 1, 1), (40, 150, 257)]
+    shapes += [(int(rng.integers(1, 41)), int(rng.integers(1, 151)), int(rng.integers(1, 601))) for _ in range(10)]
+    for M, N, K in shapes:
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K)).astype(np.float32)
+        dA, dB, dC = dev(gpu, A), dev(gpu, B), gpu.DeviceBuffer(M * N * 4)
+        gpu._check(L.qmh_matmul_nt(dA.ptr, dB.ptr, dC.ptr, M, N, K, None), "gemm")
+        assert np.array_equal(bits(dC.to_array(np.float32)), bits(oracle.gemm_nt(A, B))), (M, N, K)
+
+
+@pytest.mark.parametrize("n", [1, 7, 77, 288, 4096, 11008])
+def test_elementwise(gpu, oracle, n):
+    L = gpu.load_library()
+    x = rng.standard_normal(n).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    dx, dw, do = dev(gpu, x), dev(gpu, w), gpu.DeviceBuffer(n * 4)
+    gpu._check(L.qmh_rmsnorm(do.ptr, dx.ptr, dw.ptr, n, 1e-5, None), "rmsnorm")
+    assert np.array_equal(bits(do.to_array(np.float32)), bits(oracle.rmsnorm(x, w, 1e-5)))
+    s = (x * 6).astype(np.float32)
+    ds = dev(gpu, s)
+    gpu._check(L.qmh_softmax(ds.ptr, n, None), "softmax")
+    assert np.array_equal(bits(ds.to_array(np.float32)), bits(oracle.softmax(s)))
+    dg, du = dev(gpu, x * 8), dev(gpu, w)
+    gpu._check(L.qmh_swiglu(dg.ptr, du.ptr, n, None), "swiglu")
+    assert np.array_equal(bits(dg.to_array(np.float32)), bits(oracle.swiglu((x * 8).astype(np.float32), w)))
+    di = gpu.DeviceBuffer(4)
+    gpu._check(L.qmh_argmax(dx.ptr, n, di.ptr, None), "argmax")
+    assert di.to_array(np.int32)[0] == oracle.argmax(x)
+
+
+def test_softmax_and_argmax_known_answers(gpu):
+    L = gpu.load_library()
+    s = np.array([1000.0, 1001.0, 999.0, -1e30, 1001.0], np.float32)
+    ds = dev(gpu, s)
+    gpu._check(L.qmh_softmax(ds.ptr, 5, None), "softmax")
+    p = ds.to_array(np.float32)
+    assert abs(p.sum() - 1.0) < 1e-6 and p[1] == p[4] and p[1] > p[0] and p[3] == 0.0
+    lg = np.array([1.0, 3.0, 0.5, 2.5, -1.0, 3.0], np.float32)
+    di = gpu.DeviceBuffer(4)
+    gpu._check(L.qmh_argmax(dev(gpu, lg).ptr, 6, di.ptr, None), "argmax")
+    assert di.to_array(np.int32)[0] == 1
+    # ties across a long vector: the first index wins
+    big = np.zeros(100000, np.float32)
+    big[[777, 5000, 99999]] = 2.0
+    gpu._check(L.qmh_argmax(dev(gpu, big).ptr, big.size, di.ptr, None), "argmax")
+    assert di.to_array(np.int32)[0] == 777
+
+
+@pytest.mark.parametrize("nh,hd,pos", [(2, 12, 37), (6, 48, 255), (32, 128, 4095), (4, 64, 0)])
+def test_rope(gpu, oracle, nh, hd, pos):
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    dv = dev(gpu, v)
+    gpu._check(gpu.load_library().qmh_rope(dv.ptr, nh, hd, pos, 10000.0, None), "rope")
+    assert np.array_equal(bits(dv.to_array(np.float32)), bits(oracle.rope(v, nh, hd, pos, 10000.0)))

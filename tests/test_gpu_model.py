@@ -1,0 +1,105 @@
+"""Whole-model parity of the device forward with the CPU oracle and with the compiled
+reference (scalar ISA), through the C ABI: per-position logits bit-exact, greedy ids identical,
+prefill == sequential forwards, bad inputs rejected, bitwise run-to-run determinism."""
+import sys
+
+import numpy as np
+import pytest
+
+from _bind import ref_run
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("shape", ["small", "odd", "mha"])
+@pytest.mark.parametrize("wt", ["f32", "q8_0", "q4_0"])
+def test_forward_matches_oracle(gpu, oracle, small_models, shape, wt):
+    path = small_models[(shape, wt)]
+    say(f"case {shape}/{wt}: load {path}")
+    prompt = gpu.prompt_ids(6, 300 if shape == "mha" else 458, seed=5)
+    want, want_ids = oracle.run_model(path, prompt, n_gen=20)
+    with gpu.Model.load(path) as m:
+        got = []
+        for i, t in enumerate(prompt):
+            got.append(m.forward(int(t), i).copy())
+        tok = int(want_ids[0])
+        ids = [int(np.argmax(got[-1]))]
+        for g in range(20):
+            lg = m.forward(ids[-1], len(prompt) + g).copy()
+            got.append(lg)
+            ids.append(int(np.argmax(lg)))
+        got = np.stack(got)
+        assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
+        assert ids == list(want_ids)
+        assert tok == ids[0]
+
+
+@pytest.mark.parametrize("wt", ["f32", "q8_0", "q4_0"])
+def test_greedy_prefill_and_errors(gpu, oracle, small_models, wt):
+    path = small_models[("small", wt)]
+    prompt = gpu.prompt_ids(9, 458, seed=9)
+    want, want_ids = oracle.run_model(path, prompt, n_gen=40)
+    with gpu.Model.load(path) as m:
+        say(f"case small/{wt}: prefill")
+        lg = m.prefill(prompt, 0, want_logits=True)
+        assert np.array_equal(bits(lg), bits(want[: len(prompt)]))
+        say(f"case small/{wt}: device greedy")
+        ids = m.greedy(int(want_ids[0]), len(prompt), 40)
+        assert list(ids) == list(want_ids[1:])
+        # reference semantics: NULL on bad token / pos (src/model.c:160, tests/test_model.c:121-122)
+        assert m.forward(0, m.cfg.max_seq) is None
+        assert m.forward(m.cfg.vocab_size, 0) is None
+        assert m.forward(-1, 0) is None
+        with pytest.raises(gpu.QmhError):
+            m.greedy(0, m.cfg.max_seq - 3, 10)
+
+
+def test_rerun_is_bitwise_deterministic(gpu, small_models):
+    path = small_models[("odd", "q4_0")]
+    prompt = gpu.prompt_ids(30, 458, seed=2)
+    outs = []
+    for r in range(2):
+        with gpu.Model.load(path) as m:
+            outs.append(m.prefill(prompt, 0, want_logits=True))
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+
+
+def test_max_seq_cap(gpu, small_models):
+    with gpu.Model.load(small_models[("small", "q8_0")], max_seq=16) as m:
+        assert m.cfg.max_seq == 16
+        assert m.forward(1, 15) is not None and m.forward(1, 16) is None
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_baseline_config_vs_reference(gpu, tmp_path, name):
+    """BASELINE configs c1/c2 (stories15M shape): every position's logits bit-exact with the
+    compiled reference (scalar ISA) and the greedy ids identical over the whole decode."""
+    w = gpu.WORKLOADS[name]
+    path = str(tmp_path / f"{name}.qlm")
+    say(f"case {name}: generate")
+    gpu.gen_model(path, w.config(), w.wtype, seed=w.seed)
+    prompt = gpu.prompt_ids(w.n_prompt, w.vocab_size)
+    say(f"case {name}: reference, {w.n_prompt} prompt + {w.n_gen} greedy")
+    res, rl = ref_run(path, prompt, w.n_gen, isa="scalar", threads=4)
+    rl = rl.reshape(w.n_prompt + w.n_gen, w.vocab_size)
+    with gpu.Model.load(path) as m:
+        say(f"case {name}: device prefill")
+        lg = m.prefill(prompt, 0, want_logits=True)
+        assert np.array_equal(bits(lg), bits(rl[: w.n_prompt]))
+        say(f"case {name}: device greedy")
+        ids = m.greedy(res["tokens"][0], w.n_prompt, w.n_gen)
+        assert list(ids) == res["tokens"][1:]
+        got = []
+        toks = res["tokens"]
+        for g in range(w.n_gen):
+            got.append(m.forward(toks[g], w.n_prompt + g).copy())
+        assert np.array_equal(bits(np.stack(got)), bits(rl[w.n_prompt:]))
