@@ -130,6 +130,21 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
  * receives the argmax after each step (n_steps ids). No host round trip between steps. */
 int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
 
+/* ------------------------------------------------------------------ measurement
+ * No reference counterpart (the reference times with a host clock, bench/bench.c:11-38).
+ * Stages of one decode step: 0 = fused RMSNorm+QKV matvec (+RoPE, KV write), 1 = Wo matvec
+ * (+residual), 2 = fused RMSNorm+W1|W3 matvec (+SwiGLU), 3 = W2 matvec (+residual), 4 = final
+ * RMSNorm+output matvec, 5 = attention scores, 6 = softmax + attention-weighted V sum. */
+
+/* Average device time of `iters` back-to-back launches of one stage at position pos (token 0),
+ * from HIP events on the library stream; launch i uses layer i % n_layers, so weight reads come
+ * from HBM rather than a cache. bytes_per_launch: weight bytes one launch streams (0 for
+ * attention). Overwrites the KV cache entries at pos. */
+int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double *ms_per_launch,
+                         double *bytes_per_launch);
+/* qmh_model_greedy, with HIP events around the n_steps graph replays (*ms = their total). */
+int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms);
+
 /* ------------------------------------------------------------------ synthetic models */
 
 /* Write a random-init .qlm (format src/qlm_file.h:1-9, tensor order of the reference's

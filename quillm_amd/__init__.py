@@ -92,6 +92,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_gen_qlm": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(QmhConfig), ctypes.c_int, ctypes.c_uint64,
                                        ctypes.c_int]),
         "qmh_gen_values": (None, [ctypes.c_uint64, ctypes.c_int, i64, i64, vp]),
+        "qmh_model_time_stage": (ctypes.c_int, [vp, ctypes.c_int, i32, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                                ctypes.POINTER(ctypes.c_double)]),
+        "qmh_model_time_greedy": (ctypes.c_int, [vp, i32, i32, i32, vp, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -204,6 +207,23 @@ class Model:
         _check(load_library().qmh_model_greedy(self._h, int(token), int(pos), int(n_steps), out.ctypes.data),
                "greedy")
         return out[:n_steps]
+
+    STAGES = {"qkv": 0, "wo": 1, "w13": 2, "w2": 3, "output": 4, "attn_scores": 5, "attn_pv": 6}
+
+    def time_stage(self, stage: str, iters: int, pos: int):
+        """(ms per launch, weight bytes per launch) of one decode-step stage at position pos, from HIP events."""
+        ms, nbytes = ctypes.c_double(), ctypes.c_double()
+        _check(load_library().qmh_model_time_stage(self._h, self.STAGES[stage], int(pos), int(iters),
+                                                    ctypes.byref(ms), ctypes.byref(nbytes)), "time_stage")
+        return ms.value, nbytes.value
+
+    def time_greedy(self, token: int, pos: int, n_steps: int):
+        """(ids, device ms for the n_steps graph replays) of a device greedy run."""
+        out = np.zeros(max(n_steps, 1), np.int32)
+        ms = ctypes.c_double()
+        _check(load_library().qmh_model_time_greedy(self._h, int(token), int(pos), int(n_steps), out.ctypes.data,
+                                                     ctypes.byref(ms)), "time_greedy")
+        return out[:n_steps], ms.value
 
     def close(self):
         if self._h:

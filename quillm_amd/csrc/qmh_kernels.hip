@@ -149,8 +149,9 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
         break;
     case QMH_EPI_QKV: {
         const float partner = __shfl_xor(y, 1);
-        if (row >= a.rows) break;
         const int pos = *a.pos_ptr;
+        // the position comes from device memory: never let a stale one address past the cache
+        if (row >= a.rows || pos < 0 || pos >= a.max_seq) break;
         if (row < a.seg2) {  // q or k: rotate the (2i, 2i+1) pair, src/ops.c:114-126
             const int local = row < a.seg1 ? row : row - a.seg1;
             const int i = (local % a.head_dim) >> 1;
@@ -337,8 +338,10 @@ extern "C" int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream) {
 // ============================================================================ embedding
 
 // x = dequantised row `token` of tok_embd (src/model.c:162 -> src/quant.c:65-101)
-__global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, const int32_t *tok_ptr, float *x) {
+__global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, int vocab, const int32_t *tok_ptr,
+                        float *x) {
     const int tok = *tok_ptr;
+    if (tok < 0 || tok >= vocab) return;  // stale token in device memory: read nothing
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) {
         const int b = i >> 5, k = i & 31;
         float v;
@@ -357,10 +360,10 @@ __global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, const
     }
 }
 
-extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, const int32_t *tok_ptr, float *x,
-                                void *stream) {
+extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tok_ptr,
+                                float *x, void *stream) {
     hipLaunchKernelGGL(k_embed, dim3((dim + 255) / 256), dim3(256), 0, (hipStream_t)stream, tok_embd, dtype, dim,
-                       tok_ptr, x);
+                       vocab, tok_ptr, x);
     return (int)hipGetLastError();
 }
 
@@ -381,7 +384,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_scores(const float *__restrict_
     extern __shared__ __align__(16) uint8_t smem[];
     const int pos = *pos_ptr;
     const int t0 = blockIdx.y * QMH_ATT_TT;
-    if (t0 > pos) return;
+    if (pos < 0 || pos >= max_seq || t0 > pos) return;
     const int nt = min(QMH_ATT_TT, pos + 1 - t0);
     const int kvh = blockIdx.x, group = n_heads / n_kv, kvd = hd * n_kv;
     float *Ks = (float *)smem;                       // [QMH_ATT_TT][hd+1]
@@ -412,6 +415,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     __shared__ float redf[16];
     __shared__ float mx_s[16], inv_s[16];
     const int n = *pos_ptr + 1;
+    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
     const int kvh = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, group = n_heads / n_kv;
     float *P = (float *)smem;                      // [group][TC]
     float *Vs = P + group * QMH_PV_TC;             // [CW][TC+1]
@@ -481,7 +485,7 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vtcache, float 
 // first index of the maximum (src/sampler.c:27-32): each thread keeps the first strict
 // maximum of its stride, and pairs combine preferring the larger value, then the lower index.
 __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n, int32_t *out_idx,
-                                                 int32_t *tokpos, int32_t *record) {
+                                                 int32_t *tokpos, int32_t *record, int record_cap) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     float v = -__builtin_inff();
@@ -517,15 +521,17 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, in
         if (tokpos) {
             tokpos[0] = idx;
             tokpos[1] += 1;
-            if (record) record[tokpos[2]] = idx;
-            tokpos[2] += 1;
+            const int step = tokpos[2];
+            if (record && step >= 0 && step < record_cap) record[step] = idx;
+            tokpos[2] = step + 1;
         }
     }
 }
 
 extern "C" int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record,
-                                 void *stream) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos, record);
+                                 int record_cap, void *stream) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos, record,
+                       record_cap);
     return (int)hipGetLastError();
 }
 

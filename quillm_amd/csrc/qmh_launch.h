@@ -53,14 +53,16 @@ int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
 int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
 
-int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, const int32_t *tok_ptr, float *x, void *stream);
+int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tok_ptr, float *x,
+                     void *stream);
 int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, const int32_t *pos_ptr, int n_heads,
                            int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
                        int n_kv_heads, int head_dim, int max_seq, void *stream);
 /* argmax over x[n] -> *out_idx; if tokpos != NULL also tokpos[0] = idx, tokpos[1] += 1 and
- * record[step] = idx where step = tokpos[2]++ (device greedy loop state) */
-int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record, void *stream);
+ * record[step] = idx (when step < record_cap) where step = tokpos[2]++ (device greedy loop state) */
+int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record, int record_cap,
+                      void *stream);
 /* gate = silu(gate)*up over n (src/ops.c:128-133) */
 int qmh_launch_swiglu(float *gate, const float *up, int64_t n, void *stream);
 

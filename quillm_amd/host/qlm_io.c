@@ -1,5 +1,5 @@
 /* .qlm reader (mmap) and synthetic-model generator for the HIP host. C11. */
-#define _DEFAULT_SOURCE
+#define _GNU_SOURCE /* sincosf */
 #include "qlm_io.h"
 
 #include <fcntl.h>
@@ -238,18 +238,36 @@ static uint64_t mix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-/* element k of tensor ti: N(0,1) by Box-Muller on one 64-bit hash of (seed, ti, k) */
-static double gen_normal(uint64_t base, int64_t k) {
-    uint64_t h = mix64(base + (uint64_t)k * 0x9e3779b97f4a7c15ULL);
-    double u1 = ((double)(h >> 40) + 0.5) / 16777216.0, u2 = (double)(h & 0xffffffu) / 16777216.0;
-    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+/* Elements 2p and 2p+1 of tensor ti are the pair of N(0,1) variates Box-Muller makes from one
+ * 64-bit hash of (seed, ti, p), scaled by 0.02: r*cos(t) and r*sin(t) in fp32. */
+static void gen_pair(uint64_t base, int64_t p, float *z0, float *z1) {
+    uint64_t h = mix64(base + (uint64_t)p * 0x9e3779b97f4a7c15ULL);
+    float u1 = ((float)(h >> 40) + 0.5f) * 0x1p-24f, u2 = (float)(h & 0xffffffu) * 0x1p-24f;
+    float r = sqrtf(-2.0f * logf(u1)), s, c;
+    sincosf(6.2831853f * u2, &s, &c);
+    *z0 = 0.02f * (r * c);
+    *z1 = 0.02f * (r * s);
 }
 
 static uint64_t gen_base(uint64_t seed, int ti) { return mix64(seed ^ mix64((uint64_t)ti + 0x51ed2701ULL)); }
 
+/* out[i] = value of element k0+i */
+static void gen_fill(uint64_t base, int64_t k0, int64_t n, float *out) {
+    int64_t i = 0;
+    float a, b;
+    if (n > 0 && (k0 & 1)) { /* odd start: second half of a pair */
+        gen_pair(base, k0 >> 1, &a, &b);
+        out[i++] = b;
+    }
+    for (; i + 1 < n; i += 2) gen_pair(base, (k0 + i) >> 1, &out[i], &out[i + 1]);
+    if (i < n) {
+        gen_pair(base, (k0 + i) >> 1, &a, &b);
+        out[i] = a;
+    }
+}
+
 void qmh_gen_values(uint64_t seed, int tensor_index, int64_t k0, int64_t n, float *out) {
-    uint64_t base = gen_base(seed, tensor_index);
-    for (int64_t i = 0; i < n; i++) out[i] = (float)(0.02 * gen_normal(base, k0 + i));
+    gen_fill(gen_base(seed, tensor_index), k0, n, out);
 }
 
 typedef struct {
@@ -292,7 +310,10 @@ static void *gen_worker(void *arg) {
         size_t rb = qlm_row_bytes(t->dtype, cols);
         uint64_t base = gen_base(j->seed, (int)j->unit_tensor[u]);
         for (int64_t r = r0; r < r1; r++) {
-            for (int64_t c = 0; c < cols; c++) buf[c] = t->norm ? 1.0f : (float)(0.02 * gen_normal(base, r * cols + c));
+            if (t->norm)
+                for (int64_t c = 0; c < cols; c++) buf[c] = 1.0f;
+            else
+                gen_fill(base, r * cols, cols, buf);
             uint8_t *dst = j->data + t->off + (size_t)r * rb;
             if (t->dtype == QMH_F32) memcpy(dst, buf, (size_t)cols * 4);
             else host_quantize_row(t->dtype, buf, cols, dst);

@@ -170,7 +170,7 @@ int qmh_swiglu(float *gate, const float *up, int64_t n, void *stream) {
 int qmh_argmax(const float *x, int32_t n, int32_t *out, void *stream) {
     if (ensure()) return -1;
     if (n < 1) return fail("argmax of an empty vector");
-    LCHK(qmh_launch_argmax(x, n, out, NULL, NULL, S(stream)));
+    LCHK(qmh_launch_argmax(x, n, out, NULL, NULL, 0, S(stream)));
     return 0;
 }
 
@@ -357,15 +357,18 @@ struct qmh_model {
     hipGraphExec_t exec_fwd, exec_greedy;
 };
 
-static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
+/* the kernels of one decode step, by stage (which) and layer */
+enum { ST_QKV = 0, ST_WO = 1, ST_W13 = 2, ST_W2 = 3, ST_OUT = 4, ST_SCORES = 5, ST_PV = 6, ST_COUNT };
+
+static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     const qmh_config *c = &m->cfg;
     const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq;
     const int32_t *pos_ptr = m->d_tokpos + 1;
-    LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, D, m->d_tokpos, m->d_x, s));
-    for (int l = 0; l < c->n_layers; l++) {
-        dev_layer *L = &m->layers[l];
-        float *kl = m->d_k + (size_t)l * S_ * m->kvd, *vl = m->d_vt + (size_t)l * S_ * m->kvd;
-        qmh_mv_args a;
+    dev_layer *L = &m->layers[l];
+    float *kl = m->d_k + (size_t)l * S_ * m->kvd, *vl = m->d_vt + (size_t)l * S_ * m->kvd;
+    qmh_mv_args a;
+    switch (which) {
+    case ST_QKV: /* xb = rmsnorm(x); q,k,v = W xb; rope(q,k); k,v -> cache (src/model.c:166-173) */
         mv_args_for(&L->qkv, &a);
         a.x = m->d_x;
         a.norm_w = m->d_norms + (size_t)(2 * l) * D;
@@ -381,15 +384,19 @@ static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
         a.head_dim = m->hd;
         a.max_seq = S_;
         a.kvd = m->kvd;
-        LCHK(mv_launch(&a, s));
-        LCHK(qmh_launch_attn_scores(m->d_q, kl, m->d_att, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_,
-                                    1.0f / sqrtf((float)m->hd), s));
-        LCHK(qmh_launch_attn_pv(m->d_att, vl, m->d_xb, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_, s));
+        return mv_launch(&a, s);
+    case ST_SCORES: /* src/model.c:142-146 */
+        return qmh_launch_attn_scores(m->d_q, kl, m->d_att, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_,
+                                      1.0f / sqrtf((float)m->hd), s);
+    case ST_PV: /* src/model.c:147-154 */
+        return qmh_launch_attn_pv(m->d_att, vl, m->d_xb, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_, s);
+    case ST_WO: /* x += Wo xb (src/model.c:178-179) */
         mv_args_for(&L->wo, &a);
         a.x = m->d_xb;
         a.epi = QMH_EPI_ADD;
         a.out0 = m->d_x;
-        LCHK(mv_launch(&a, s));
+        return mv_launch(&a, s);
+    case ST_W13: /* hb = silu(W1 rmsnorm(x)) * (W3 rmsnorm(x)) (src/model.c:181-184) */
         mv_args_for(&L->w13, &a);
         a.x = m->d_x;
         a.norm_w = m->d_norms + (size_t)(2 * l + 1) * D;
@@ -397,27 +404,105 @@ static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
         a.out0 = m->d_hb;
         if (L->w13.dtype == QMH_F32) {
             a.epi = QMH_EPI_STORE;
-            LCHK(mv_launch(&a, s));
-            LCHK(qmh_launch_swiglu(m->d_hb, m->d_hb + H, H, s));
-        } else {
-            a.epi = QMH_EPI_SWIGLU;
-            LCHK(mv_launch(&a, s));
+            int rc = mv_launch(&a, s);
+            return rc ? rc : qmh_launch_swiglu(m->d_hb, m->d_hb + H, H, s);
         }
+        a.epi = QMH_EPI_SWIGLU;
+        return mv_launch(&a, s);
+    case ST_W2: /* x += W2 hb (src/model.c:185-186) */
         mv_args_for(&L->w2, &a);
         a.x = m->d_hb;
         a.epi = QMH_EPI_ADD;
         a.out0 = m->d_x;
-        LCHK(mv_launch(&a, s));
+        return mv_launch(&a, s);
+    case ST_OUT: /* logits = Woutput rmsnorm(x) (src/model.c:188-189) */
+        mv_args_for(&m->output, &a);
+        a.x = m->d_x;
+        a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
+        a.eps = c->norm_eps;
+        a.epi = QMH_EPI_STORE;
+        a.out0 = m->d_logits;
+        return mv_launch(&a, s);
     }
-    qmh_mv_args a;
-    mv_args_for(&m->output, &a);
-    a.x = m->d_x;
-    a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
-    a.eps = c->norm_eps;
-    a.epi = QMH_EPI_STORE;
-    a.out0 = m->d_logits;
-    LCHK(mv_launch(&a, s));
-    if (with_argmax) LCHK(qmh_launch_argmax(m->d_logits, c->vocab_size, NULL, m->d_tokpos, m->d_record, s));
+    return (int)hipErrorInvalidValue;
+}
+
+static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
+    const qmh_config *c = &m->cfg;
+    LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, c->dim, c->vocab_size, m->d_tokpos, m->d_x, s));
+    static const int order[6] = {ST_QKV, ST_SCORES, ST_PV, ST_WO, ST_W13, ST_W2};
+    for (int l = 0; l < c->n_layers; l++)
+        for (int k = 0; k < 6; k++) LCHK(enqueue_stage(m, order[k], l, s));
+    LCHK(enqueue_stage(m, ST_OUT, 0, s));
+    if (with_argmax)
+        LCHK(qmh_launch_argmax(m->d_logits, c->vocab_size, NULL, m->d_tokpos, m->d_record, c->max_seq, s));
+    return 0;
+}
+
+/* weight bytes one launch of a stage streams (the algorithmic bytes of the matvecs) */
+static double stage_weight_bytes(const qmh_model *m, int which) {
+    const struct qmh_weight *w = which == ST_QKV ? &m->layers[0].qkv
+                                 : which == ST_WO ? &m->layers[0].wo
+                                 : which == ST_W13 ? &m->layers[0].w13
+                                 : which == ST_W2 ? &m->layers[0].w2
+                                 : which == ST_OUT ? &m->output
+                                                   : NULL;
+    if (!w) return 0.0;
+    const double rows = which == ST_W13 ? 2.0 * (double)w->rows : (double)w->rows;
+    return rows * (double)qlm_row_bytes(w->dtype, w->cols);
+}
+
+int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double *ms_per_launch,
+                         double *bytes_per_launch) {
+    if (!m || which < 0 || which >= ST_COUNT || iters < 1 || pos < 0 || pos >= m->cfg.max_seq)
+        return fail("time_stage: bad arguments");
+    /* the stages read token and position from device memory: set both (a greedy run leaves
+     * the position one past its last step) */
+    int32_t *slot = m->h_tokpos;
+    slot[0] = 0, slot[1] = pos;
+    HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream));
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    int rc = 0;
+    hipError_t e = hipEventRecord(e0, g_stream);
+    for (int i = 0; i < iters && e == hipSuccess && rc == 0; i++)
+        rc = enqueue_stage(m, which, which == ST_OUT ? 0 : i % m->cfg.n_layers, g_stream);
+    if (e == hipSuccess && rc == 0) e = hipEventRecord(e1, g_stream);
+    if (e == hipSuccess && rc == 0) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess && rc == 0) e = hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc) return fail("time_stage launch: %s", hipGetErrorString((hipError_t)rc));
+    if (e != hipSuccess) return fail("time_stage: %s", hipGetErrorString(e));
+    if (ms_per_launch) *ms_per_launch = (double)ms / iters;
+    if (bytes_per_launch) *bytes_per_launch = stage_weight_bytes(m, which);
+    return 0;
+}
+
+int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms) {
+    if (!m || n_steps < 1 || token < 0 || token >= m->cfg.vocab_size || pos < 0 ||
+        (int64_t)pos + n_steps > m->cfg.max_seq)
+        return fail("time_greedy: bad token/range");
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    int32_t *slot = m->h_tokpos;
+    slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
+    hipError_t e = hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, g_stream);
+    for (int32_t k = 0; k < n_steps && e == hipSuccess; k++) e = hipGraphLaunch(m->exec_greedy, g_stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, g_stream);
+    if (e == hipSuccess && out)
+        e = hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (e != hipSuccess) return fail("time_greedy: %s", hipGetErrorString(e));
+    if (ms) *ms = (double)t;
     return 0;
 }
 

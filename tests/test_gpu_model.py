@@ -73,6 +73,23 @@ def test_rerun_is_bitwise_deterministic(gpu, small_models):
     assert np.array_equal(bits(outs[0]), bits(outs[1]))
 
 
+def test_stage_timing_after_greedy_to_end_of_context(gpu, oracle, small_models):
+    """A greedy run that fills the context leaves the device position one past the end; the
+    stage timer must set its own position (regression: it used the stale one)."""
+    path = small_models[("small", "q8_0")]
+    with gpu.Model.load(path, max_seq=24) as m:
+        m.prefill(gpu.prompt_ids(8, 458, seed=4), 0)
+        m.greedy(3, 8, 16)  # positions 8..23: the device position ends at 24 == max_seq
+        for st in m.STAGES:
+            ms, nbytes = m.time_stage(st, 4, pos=23)
+            assert ms > 0
+        with pytest.raises(gpu.QmhError):
+            m.time_stage("qkv", 1, pos=24)
+        lg = m.forward(5, 0)
+        want, _ = oracle.run_model(path, [5], n_gen=0, max_seq=24)
+        assert np.array_equal(bits(lg), bits(want[0]))
+
+
 def test_max_seq_cap(gpu, small_models):
     with gpu.Model.load(small_models[("small", "q8_0")], max_seq=16) as m:
         assert m.cfg.max_seq == 16
