@@ -1,0 +1,165 @@
+// gfx950 attention kernels of the quillm token loop (decode: one query position).
+//
+// Reference src/model.c:127-156, per head h (kv head h/group):
+//   att[t] = dot_f32(q_h, K[t]) * scale      serial fp32 dot over head_dim (src/kernels_scalar.c:6-10)
+//   softmax(att[0..pos])                     max, expf, double sum, * (float)(1/sum) (src/ops.c:100-112)
+//   out[i] = +0; out[i] = out[i] + att[t]*V[t][i] for t = 0..pos in order
+// Both float sums keep that order: a score is one lane's chain over head_dim, an output
+// element one lane's chain over positions. The caches are laid out for those chains:
+//   K: [kvd][max_seq] per layer (transposed): lanes = positions read consecutive floats;
+//   V: [max_seq][kvd] per layer: a position's row is contiguous.
+// The softmax's double sum is a fixed tree (see qmh_block_sum_d); it can differ from the
+// reference's serial double sum in its last bits, which the fp32 1/sum absorbs unless the
+// two straddle an fp32 rounding boundary.
+#include "qmh_device.h"
+#include "qmh_launch.h"
+
+// ============================================================================ scores
+
+#define QMH_SC_T 64  // positions per workgroup (one wave, one position per lane)
+
+// HD > 0: head_dim known at compile time -- all HD loads of a lane are issued before its chain
+// starts (maximum bytes in flight); HD == 0: any head_dim, loads in groups of 16. The query
+// is read with uniform (scalar) loads: every lane of the wave needs the same q values.
+template <int HD>
+__global__ __launch_bounds__(QMH_SC_T) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ Kt,
+                                                          float *__restrict__ att, const int32_t *pos_ptr,
+                                                          int n_heads, int n_kv, int hd_rt, int max_seq, float scale) {
+    const int hd = HD > 0 ? HD : hd_rt;
+    const int pos = *pos_ptr;
+    const int t0 = blockIdx.y * QMH_SC_T;
+    if (pos < 0 || pos >= max_seq || t0 > pos) return;
+    const int kvh = blockIdx.x, group = n_heads / n_kv;
+    const int t = t0 + (int)threadIdx.x;
+    const int tc = t < max_seq ? t : max_seq - 1;  // in-bounds position for the loads
+    const float *kcol = Kt + (size_t)kvh * hd * max_seq + tc;
+    if (HD > 0) {
+        float kv[HD > 0 ? HD : 1];
+#pragma unroll
+        for (int i = 0; i < HD; i++) kv[i] = kcol[(size_t)i * max_seq];
+        for (int hl = 0; hl < group; hl++) {
+            const float *qh = q + (size_t)(kvh * group + hl) * HD;
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD; i++) s = s + qh[i] * kv[i];
+            if (t <= pos) att[(size_t)(kvh * group + hl) * max_seq + t] = s * scale;
+        }
+    } else {
+        for (int hl = 0; hl < group; hl++) {
+            const float *qh = q + (size_t)(kvh * group + hl) * hd;
+            float s = 0.0f;
+            for (int i0 = 0; i0 < hd; i0 += 16) {
+                float kv[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) kv[k] = kcol[(size_t)(i0 + k < hd ? i0 + k : hd - 1) * max_seq];
+#pragma unroll
+                for (int k = 0; k < 16; k++)
+                    if (i0 + k < hd) s = s + qh[i0 + k] * kv[k];
+            }
+            if (t <= pos) att[(size_t)(kvh * group + hl) * max_seq + t] = s * scale;
+        }
+    }
+}
+
+extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, const int32_t *pos_ptr,
+                                      int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void *stream) {
+    dim3 grid(n_kv_heads, (max_seq + QMH_SC_T - 1) / QMH_SC_T);
+    hipStream_t s = (hipStream_t)stream;
+#define QMH_SC(HD) \
+    hipLaunchKernelGGL(k_attn_scores<HD>, grid, dim3(QMH_SC_T), 0, s, q, kcache, att, pos_ptr, n_heads, n_kv_heads, \
+                       head_dim, max_seq, scale)
+    if (head_dim == 128) QMH_SC(128);
+    else if (head_dim == 64) QMH_SC(64);
+    else if (head_dim == 48) QMH_SC(48);
+    else QMH_SC(0);
+#undef QMH_SC
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ softmax + V sum
+
+#define QMH_PV_CW 16   // output columns per workgroup
+#define QMH_PV_TC 256  // positions per LDS chunk
+#define QMH_PV_VS (QMH_PV_TC + 4)  // LDS row stride of the V chunk (== 4 mod 64 floats)
+
+__global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ att, const float *__restrict__ V,
+                                                    float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
+                                                    int n_kv, int hd, int max_seq) {
+    __shared__ __align__(16) float P[16 * QMH_PV_TC];          // [group][TC] probabilities
+    __shared__ __align__(16) float Vs[QMH_PV_CW * QMH_PV_VS];  // [CW][TC] the chunk, transposed
+    __shared__ double red[16];
+    __shared__ float redf[16];
+    __shared__ float mx_s[16], inv_s[16];
+    const int n = *pos_ptr + 1;
+    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
+    const int kvh = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, group = n_heads / n_kv, kvd = hd * n_kv;
+    // softmax statistics per head of the group (src/ops.c:100-112)
+    for (int hl = 0; hl < group; hl++) {
+        const float *s = att + (size_t)(kvh * group + hl) * max_seq;
+        float m = -__builtin_inff();
+        for (int t = threadIdx.x; t < n; t += QMH_WG) m = s[t] > m ? s[t] : m;
+        m = qmh_block_max(m, redf);
+        double sum = 0.0;
+        for (int t = threadIdx.x; t < n; t += QMH_WG) sum += (double)qmh_expf(s[t] - m);
+        sum = qmh_block_sum_d(sum, red);
+        if (threadIdx.x == 0) {
+            mx_s[hl] = m;
+            inv_s[hl] = (float)(1.0 / sum);
+        }
+    }
+    __syncthreads();
+    const int lane_h = threadIdx.x / QMH_PV_CW, col = threadIdx.x % QMH_PV_CW;
+    const bool chain = lane_h < group;
+    const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
+    constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < n; t0 += QMH_PV_TC) {
+        const int nt = min(QMH_PV_TC, n - t0);
+        // the chunk's V values: unconditional, clamped loads, all in flight together
+        float vv[LPT];
+#pragma unroll
+        for (int k = 0; k < LPT; k++) {
+            const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW;
+            const int tcl = t0 + t < n ? t0 + t : n - 1;
+            vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];
+        }
+        // probabilities of the chunk, +0 past nt
+        for (int e = threadIdx.x; e < group * QMH_PV_TC; e += QMH_WG) {
+            const int hl = e / QMH_PV_TC, t = e % QMH_PV_TC;
+            float p = 0.0f;
+            if (t < nt) p = qmh_expf(att[(size_t)(kvh * group + hl) * max_seq + t0 + t] - mx_s[hl]) * inv_s[hl];
+            P[hl * QMH_PV_TC + t] = p;
+        }
+#pragma unroll
+        for (int k = 0; k < LPT; k++) {
+            const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW, cc = e % QMH_PV_CW;
+            Vs[cc * QMH_PV_VS + t] = t < nt ? vv[k] : 0.0f;
+        }
+        __syncthreads();
+        if (chain) {
+            // out = out + p_t*v_t in t order; the chunk is zero past nt (p*0 = +0 and the sum,
+            // which started at +0, is never -0, so the extra terms change nothing)
+            const float4 *p4 = (const float4 *)(P + lane_h * QMH_PV_TC), *v4 = (const float4 *)(Vs + col * QMH_PV_VS);
+            const int n4 = (nt + 3) >> 2;
+            for (int k = 0; k < n4; k++) {
+                const float4 p = p4[k], v = v4[k];
+                acc = acc + p.x * v.x;
+                acc = acc + p.y * v.y;
+                acc = acc + p.z * v.z;
+                acc = acc + p.w * v.w;
+            }
+        }
+        __syncthreads();
+    }
+    if (chain && i0 + col < hd) out[(size_t)(kvh * group + lane_h) * hd + i0 + col] = acc;
+}
+
+extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *out, const int32_t *pos_ptr,
+                                  int n_heads, int n_kv_heads, int head_dim, int max_seq, void *stream) {
+    const int group = n_heads / n_kv_heads;
+    if (group > 16 || group * QMH_PV_CW > QMH_WG) return (int)hipErrorInvalidValue;
+    dim3 grid(n_kv_heads, (head_dim + QMH_PV_CW - 1) / QMH_PV_CW);
+    hipLaunchKernelGGL(k_attn_pv, grid, dim3(QMH_WG), 0, (hipStream_t)stream, att, vcache, out, pos_ptr, n_heads,
+                       n_kv_heads, head_dim, max_seq);
+    return (int)hipGetLastError();
+}

@@ -13,6 +13,8 @@ extern "C" {
 
 /* rows per tile of the device weight layout */
 #define QMH_TILE_R 16
+/* slots of padding after a quantized weight's tiles: >= one matvec chunk (256 threads x 8 blocks) */
+#define QMH_WEIGHT_PAD_SLOTS 4096
 
 /* matvec epilogues */
 enum {
@@ -50,6 +52,8 @@ typedef struct {
 int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes, uint16_t *scales,
                       int tile_r, int64_t row_off, int interleave_half, void *stream);
 int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
+/* dynamic LDS bytes the quantized matvec needs (must be <= 64 KiB) */
+size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
 int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
 

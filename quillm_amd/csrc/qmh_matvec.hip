@@ -1,0 +1,461 @@
+// gfx950 matrix-vector kernels of the quillm token loop (Q4_0 / Q8_0 / f32 weights).
+//
+// Rounding contract: results are bit-identical to the reference's scalar CPU path. The
+// int32 block dots are exact in any order; every float sum keeps the reference's order
+// (one serial chain per row), so parallelism comes from rows and blocks, never from
+// re-associating a float sum. Built with -ffp-contract=off (no a*b+c fusion).
+#include "qmh_device.h"
+#include "qmh_launch.h"
+
+#define QMH_Q8 2
+#define QMH_Q4 3
+
+// ============================================================================ weight tiles
+//
+// Device layout of a quantized weight (one allocation each for codes and scales):
+//   tile t covers tile_r rows; inside a tile, block b of row r sits at slot
+//   s = (t*nb + b)*tile_r + r;  codes at s*CB bytes (CB = 16 for Q4_0, 32 for Q8_0),
+//   scale (the block's fp16 d) at scales[s].
+// A wave reading consecutive slots reads consecutive 16/32-byte code chunks (coalesced
+// dwordx4 loads). Values are the .qlm bytes, only moved.
+
+__global__ void k_repack(const uint8_t *__restrict__ src, int64_t src_rows, int nb, int bs, int cb,
+                         uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int tile_r, int64_t row_off,
+                         int half) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= src_rows * nb) return;
+    int64_t row = idx / nb;
+    int b = (int)(idx % nb);
+    const uint8_t *blk = src + (row * nb + b) * bs;
+    int64_t tile, r;
+    if (half < 0) {  // rows appended at row_off
+        int64_t g = row_off + row;
+        tile = g / tile_r;
+        r = g % tile_r;
+    } else {  // two matrices interleaved per tile: first half rows, then second half rows
+        int hr = tile_r / 2;
+        tile = row / hr;
+        r = row % hr + (int64_t)half * hr;
+    }
+    int64_t slot = (tile * nb + b) * tile_r + r;
+    scales[slot] = (uint16_t)(blk[0] | (blk[1] << 8));
+    uint8_t *dst = codes + slot * cb;
+    for (int i = 0; i < cb; i++) dst[i] = blk[2 + i];
+}
+
+extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes,
+                                 uint16_t *scales, int tile_r, int64_t row_off, int interleave_half, void *stream) {
+    int bs = dtype == QMH_Q4 ? 18 : 34, cb = dtype == QMH_Q4 ? 16 : 32;
+    int64_t total = src_rows * nb;
+    if (total <= 0) return 0;
+    int64_t grid = (total + 255) / 256;
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, src, src_rows, nb, bs, cb,
+                       codes, scales, tile_r, row_off, interleave_half);
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ activation
+//
+// Every matvec workgroup turns the f32 activation into Q8_0 blocks in its own LDS (the
+// reference quantizes x once per qm_matvec, src/ops.c:59; the result is the same wherever it
+// is computed). With RMSNorm (NORM) the gain is applied first (src/ops.c:93-98), so the
+// normalised vector never round-trips through memory. The activation is read into registers
+// with unconditional, index-clamped loads issued BEFORE the weight loads (the vector-memory
+// counter retires loads in order, so the prologue never waits for weights), then staged in
+// LDS and quantized:
+//   acodes[b*32 + k]: the block's 32 codes. For Q4_0 weights they are stored split, even
+//                     elements in [0,16) and odd elements in [16,32), to match the weight's
+//                     low/high nibbles; asum[b] = sum of the codes.
+//   ad[b]            : fp32(fp16(d)) of the block.
+
+template <bool NORM>
+struct ActRegs {
+    static constexpr int XR = NORM ? 24 : 48;  // x values per thread: n <= XR*256
+    static constexpr int WR = NORM ? 24 : 1;   // gain values per thread
+};
+
+template <bool SPLIT, bool NORM>
+__device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *wr, int8_t *acodes, float *ad,
+                           int *asum, double *red, float *stage) {
+    constexpr int XR = ActRegs<NORM>::XR;
+    const int n = a.cols, nb = a.nb, n32 = nb * 32;
+    float *xs = stage, *ws = stage + n32;
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const int i = k * QMH_WG + (int)threadIdx.x;
+        if (i < n32) {
+            const float xv = i < n ? xr[k] : 0.0f;
+            xs[i] = xv;
+            if (NORM) ws[i] = i < n ? wr[k] : 0.0f;
+            ss += (double)xv * (double)xv;
+        }
+    }
+    float inv = 1.0f;
+    if (NORM) {
+        ss = qmh_block_sum_d(ss, red);  // its barriers also publish xs/ws
+        inv = (float)(1.0 / sqrt(ss / (double)n + (double)a.eps));
+    } else {
+        __syncthreads();
+    }
+    const int sub = threadIdx.x & 7;
+    const int per_pass = QMH_WG >> 3;
+    for (int b0 = 0; b0 < nb; b0 += per_pass) {
+        const int b = b0 + (threadIdx.x >> 3);
+        const bool on = b < nb;
+        const int i4 = (on ? b : 0) * 32 + sub * 4;
+        const float4 x4 = *(const float4 *)(xs + i4);
+        float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (NORM) w4 = *(const float4 *)(ws + i4);
+        const float xa[4] = {x4.x, x4.y, x4.z, x4.w}, wa[4] = {w4.x, w4.y, w4.z, w4.w};
+        float v[4], m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float xv = (on && i4 + k < n) ? xa[k] : 0.0f;
+            if (NORM) xv = xv * inv * wa[k];  // (x*inv)*w as the reference; 0 stays 0 past n
+            v[k] = xv;
+            const float av = fabsf(xv);
+            m = av > m ? av : m;
+        }
+        m = qmh_amax8(m);
+        const uint16_t dh = qmh_f2h(m / 127.0f);
+        const float dd = qmh_h2f(dh);
+        int q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = qmh_q8_code(v[k], dd);
+        int ps = q[0] + q[1] + q[2] + q[3];
+        ps += __shfl_xor(ps, 1);
+        ps += __shfl_xor(ps, 2);
+        ps += __shfl_xor(ps, 4);
+        if (on) {
+            int8_t *c = acodes + b * 32;
+            if (SPLIT) {
+                c[sub * 2 + 0] = (int8_t)q[0];
+                c[sub * 2 + 1] = (int8_t)q[2];
+                c[16 + sub * 2 + 0] = (int8_t)q[1];
+                c[16 + sub * 2 + 1] = (int8_t)q[3];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) c[sub * 4 + k] = (int8_t)q[k];
+            }
+            if (sub == 0) {
+                ad[b] = dd;
+                asum[b] = ps;
+            }
+            if (a.xq_out && blockIdx.x == 0) {
+                uint8_t *o = a.xq_out + (size_t)b * 34;
+                if (sub == 0) {
+                    o[0] = (uint8_t)(dh & 0xff);
+                    o[1] = (uint8_t)(dh >> 8);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)q[k];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ============================================================================ epilogue
+
+// Values an epilogue reads from memory, fetched before the next chunk's weight loads.
+struct EpiIn {
+    float resid;  // EPI_ADD: the residual x[row]
+    float c, s;   // EPI_QKV: RoPE factors of the row's pair at pos
+};
+
+__device__ __forceinline__ EpiIn epi_fetch(const qmh_mv_args &a, int row, int pos) {
+    EpiIn e = {0.0f, 1.0f, 0.0f};
+    const int rc = row < a.rows ? row : a.rows - 1;
+    if (a.epi == QMH_EPI_ADD) e.resid = a.out0[rc];
+    if (a.epi == QMH_EPI_QKV) {
+        const int local = rc < a.seg1 ? rc : (rc < a.seg2 ? rc - a.seg1 : 0);
+        const int i = (local % a.head_dim) >> 1;
+        const int p = pos < 0 ? 0 : (pos >= a.max_seq ? a.max_seq - 1 : pos);
+        const float2 cs = *(const float2 *)(a.rope + ((size_t)p * (a.head_dim >> 1) + i) * 2);
+        e.c = cs.x;
+        e.s = cs.y;
+    }
+    return e;
+}
+
+// y: the row's result. Lanes of one tile hold consecutive rows, so the RoPE partner of row
+// 2i/2i+1 is lane ^ 1 and the W3 partner of an interleaved W1 row is lane + 16.
+// K goes to a transposed cache [kvd][max_seq], V to a row cache [max_seq][kvd].
+__device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float y, int lane, int pos,
+                                            const EpiIn &e) {
+    switch (a.epi) {
+    case QMH_EPI_STORE:
+        if (row < a.rows) a.out0[row] = y;
+        break;
+    case QMH_EPI_ADD:  // x[i] += y[i] (src/model.c:179,186)
+        if (row < a.rows) a.out0[row] = e.resid + y;
+        break;
+    case QMH_EPI_QKV: {
+        const float partner = __shfl_xor(y, 1);
+        // the position comes from device memory: never let a stale one address past the cache
+        if (row >= a.rows || pos < 0 || pos >= a.max_seq) break;
+        if (row < a.seg2) {  // q or k: rotate the (2i, 2i+1) pair, src/ops.c:114-126
+            const int local = row < a.seg1 ? row : row - a.seg1;
+            const float v = (local & 1) == 0 ? (y * e.c - partner * e.s) : (partner * e.s + y * e.c);
+            if (row < a.seg1) a.out0[local] = v;
+            else a.out1[(size_t)local * a.max_seq + pos] = v;
+        } else {
+            a.out2[(size_t)pos * a.kvd + (row - a.seg2)] = y;
+        }
+        break;
+    }
+    case QMH_EPI_SWIGLU: {  // silu(g)*u (src/ops.c:128-133)
+        const float up = __shfl_down(y, 16);
+        if (lane < 16 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf(-y)) * up;
+        break;
+    }
+    }
+}
+
+// The serial chain of one row: s = +0; s = s + t[b] for b = 0..nb-1, reading the row as
+// float4s with the next 8 float4s in flight while the current 32 terms are added. The row is
+// zero past nb (adding +0 to a sum that started at +0 changes nothing: such a sum is never
+// -0) and reads stay inside the row's LDS stride.
+__device__ __forceinline__ float mv_chain(const float *row, int nb) {
+    const float4 *r4 = (const float4 *)row;
+    const int n4 = (nb + 3) >> 2;
+    float s = 0.0f;
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = r4[k < n4 ? k : 0];
+    for (int k0 = 0; k0 < n4; k0 += 8) {
+        float4 w[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) w[k] = r4[k0 + 8 + k < n4 ? k0 + 8 + k : 0];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (k0 + k < n4) {
+                s = s + v[k].x;
+                s = s + v[k].y;
+                s = s + v[k].z;
+                s = s + v[k].w;
+            }
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = w[k];
+    }
+    return s;
+}
+
+// ============================================================================ quantized matvec
+//
+// y = W x with W Q4_0 or Q8_0 and x quantized to Q8_0 (src/ops.c:36-61), one row's dot as in
+// src/kernels_scalar.c:12-34:  s = +0; for b: s = s + (float)acc_b * (d_w,b * d_x,b).
+//
+// Workgroup = 256 threads, grid-stride over tiles of R rows, tile = R*nb blocks cut into
+// chunks of 256*CH blocks (thread tid owns blocks l = chunk*256*CH + k*256 + tid). Per chunk:
+//   1. the NEXT chunk's code/scale loads are issued first (two register buffers used
+//      alternately; the allocation is padded so these loads are unconditional and the
+//      compiler waits for exactly the older chunk),
+//   2. the exact int32 block dot against the LDS activation and the term
+//      t = (float)acc * (d_w*d_x) go to T[r][b] in LDS,
+//   3. after the tile's last chunk, lanes 0..R-1 run each row's serial chain, then the
+//      epilogue.
+
+// LDS row stride of T: >= nb rounded up to 4, and == 4 mod 64 floats so the chain lanes'
+// float4 reads and the compute phase's writes fall in distinct banks
+__host__ __device__ __forceinline__ int mv_tstride(int nb) {
+    const int nb4 = (nb + 3) & ~3;
+    return nb4 + (((4 - nb4) % 64) + 64) % 64;
+}
+
+// dynamic LDS bytes of k_matvec for (nb, R, with RMSNorm prologue or not)
+__host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, bool norm) {
+    const size_t t = (size_t)R * mv_tstride(nb), st = (size_t)(norm ? 2 : 1) * nb * 32;
+    return (size_t)nb * 40 + 4 * (t > st ? t : st);
+}
+
+template <int WT, int R, bool NORM>
+__global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
+    constexpr int CB = WT == QMH_Q4 ? 16 : 32;  // code bytes per block
+    constexpr int NV = CB / 16;                 // uint4 per block
+    constexpr int CH = WT == QMH_Q4 ? 8 : 4;    // blocks per thread per chunk
+    constexpr int CHUNK = QMH_WG * CH;
+    constexpr int XR = ActRegs<NORM>::XR, WR = ActRegs<NORM>::WR;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[16];
+
+    const int nb = a.nb, TB = R * nb, nchunk = (TB + CHUNK - 1) / CHUNK, S = mv_tstride(nb);
+    const int tid = threadIdx.x, n = a.cols;
+    int tile = blockIdx.x;
+    if (tile >= a.ntiles) return;
+
+    int8_t *acodes = (int8_t *)smem;
+    float *ad = (float *)(smem + (size_t)nb * 32);
+    int *asum = (int *)(smem + (size_t)nb * 36);
+    float *T = (float *)(smem + (size_t)nb * 40);  // [R][S]; first the activation's staging area
+
+    // 1. activation (and gain) loads, unconditional with clamped indices
+    float xr[XR], wr[WR];
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const int i = k * QMH_WG + tid;
+        xr[k] = a.x[i < n ? i : n - 1];
+    }
+    if (NORM) {
+#pragma unroll
+        for (int k = 0; k < WR; k++) {
+            const int i = k * QMH_WG + tid;
+            wr[k] = a.norm_w[i < n ? i : n - 1];
+        }
+    }
+    const int pos = a.pos_ptr ? *a.pos_ptr : 0;
+
+    const uint4 *codes = (const uint4 *)a.codes;
+    uint4 A[CH][NV], B[CH][NV];
+    uint32_t As[CH], Bs[CH];
+
+#define QMH_LOAD(BUF, BS, TILE, CHK)                                                           \
+    {                                                                                          \
+        const size_t base = (size_t)(TILE) * TB + (size_t)(CHK) * CHUNK + tid;                 \
+        _Pragma("unroll") for (int k = 0; k < CH; k++) {                                       \
+            const size_t slot = base + (size_t)k * QMH_WG;                                     \
+            _Pragma("unroll") for (int v = 0; v < NV; v++) BUF[k][v] = codes[slot * NV + v];   \
+            BS[k] = a.scales[slot];                                                            \
+        }                                                                                      \
+    }
+
+#define QMH_COMPUTE(BUF, BS, CHK)                                                                        \
+    _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
+        const int l = (CHK) * CHUNK + k * QMH_WG + tid;                                                  \
+        if (l < TB) {                                                                                    \
+            const int b = l / R, r = l % R;                                                              \
+            const int4 *xv = (const int4 *)(acodes + b * 32);                                            \
+            const int4 x0 = xv[0], x1 = xv[1];                                                           \
+            int acc = 0;                                                                                 \
+            if (WT == QMH_Q4) {                                                                          \
+                const uint4 w = BUF[k][0];                                                               \
+                acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);                \
+                acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);         \
+                acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);                \
+                acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);         \
+                acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);                \
+                acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);         \
+                acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);                \
+                acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);         \
+                acc -= 8 * asum[b]; /* sum (q-8)*x = sum q*x - 8*sum x, exact */                         \
+            } else {                                                                                     \
+                const uint4 w0 = BUF[k][0], w1 = BUF[k][NV - 1];                                         \
+                acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);                               \
+                acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);                               \
+            }                                                                                            \
+            T[r * S + b] = (float)acc * (qmh_h2f((uint16_t)BS[k]) * ad[b]);                              \
+        }                                                                                                \
+    }
+
+    // one step: epilogue inputs (tile's last chunk only), then the loads of the chunk after
+    // (tile, c) into NXT, then compute CUR and finish the tile. When nothing follows, NXT
+    // re-reads the current chunk (an L2 hit) so the loads stay unconditional.
+#define QMH_STEP(CUR, CURS, NXT, NXTS)                                                         \
+    {                                                                                          \
+        int nt = tile, nc = c + 1;                                                             \
+        if (nc == nchunk) {                                                                    \
+            nt = tile + gridDim.x;                                                             \
+            nc = 0;                                                                            \
+        }                                                                                      \
+        more = nt < a.ntiles;                                                                  \
+        const int row = R == QMH_TILE_R ? tile * R + (tid & (R - 1))                           \
+                                        : tile * (R / 2) + (tid & (R / 2 - 1));                \
+        EpiIn ein = {0.0f, 1.0f, 0.0f};                                                        \
+        if (c == nchunk - 1) ein = epi_fetch(a, row, pos);                                     \
+        QMH_LOAD(NXT, NXTS, more ? nt : tile, more ? nc : c);                                  \
+        QMH_COMPUTE(CUR, CURS, c);                                                             \
+        if (c == nchunk - 1) {                                                                 \
+            __syncthreads();                                                                   \
+            if (tid < R) mv_epilogue(a, row, mv_chain(T + tid * S, nb), tid, pos, ein);        \
+            __syncthreads();                                                                   \
+        }                                                                                      \
+        tile = nt;                                                                             \
+        c = nc;                                                                                \
+    }
+
+    // 2. first weight chunk, then 3. the activation into LDS while it is in flight
+    QMH_LOAD(A, As, tile, 0);
+    act_finish<WT == QMH_Q4, NORM>(a, xr, wr, acodes, ad, asum, red, T);
+    // zero T once: the chain adds whole float4s, the pad past nb must read +0
+    for (int i = tid; i < R * S; i += QMH_WG) T[i] = 0.0f;
+    __syncthreads();
+
+    int c = 0;
+    bool more = true;
+    for (;;) {
+        QMH_STEP(A, As, B, Bs);
+        if (!more) break;
+        QMH_STEP(B, Bs, A, As);
+        if (!more) break;
+    }
+#undef QMH_STEP
+#undef QMH_COMPUTE
+#undef QMH_LOAD
+}
+
+// f32 weights (src/kernels_scalar.c:6-10 via src/ops.c:42-45): lane per row, x in LDS,
+// s = +0; s = s + w_i*x_i in index order.
+__global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[16];
+    float *xs = (float *)smem;
+    const int n = a.cols;
+    float inv = 1.0f;
+    if (a.norm_w) {
+        double ss = 0.0;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            double v = (double)a.x[i];
+            ss += v * v;
+        }
+        ss = qmh_block_sum_d(ss, red);
+        inv = (float)(1.0 / sqrt(ss / (double)n + (double)a.eps));
+    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = a.norm_w ? a.x[i] * inv * a.norm_w[i] : a.x[i];
+    __syncthreads();
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    const float *w = (const float *)a.codes + (size_t)(row < a.rows ? row : 0) * n;
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s = s + w[i] * xs[i];
+    const int pos = a.pos_ptr ? *a.pos_ptr : 0;
+    const EpiIn e = epi_fetch(a, row, pos);
+    mv_epilogue(a, row, s, threadIdx.x & 15, pos, e);
+}
+
+extern "C" size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm) { return mv_lds_bytes(nb, tile_r, norm != 0); }
+
+extern "C" int qmh_matvec_max_cols(int norm) { return ActRegs<true>::XR * QMH_WG * (norm ? 1 : 2); }
+
+extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream) {
+    const int grid = a->ntiles < grid_cap ? a->ntiles : grid_cap;
+    const bool norm = a->norm_w != NULL;
+    const size_t lds = mv_lds_bytes(a->nb, a->tile_r, norm);
+    if (lds > 65536 || a->cols > qmh_matvec_max_cols(norm) || a->cols < 1) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+#define QMH_MV(WT, R, N) hipLaunchKernelGGL((k_matvec<WT, R, N>), dim3(grid), dim3(QMH_WG), lds, s, *a)
+    if (a->dtype == QMH_Q4 && a->tile_r == 16) {
+        if (norm) QMH_MV(QMH_Q4, 16, true); else QMH_MV(QMH_Q4, 16, false);
+    } else if (a->dtype == QMH_Q4 && a->tile_r == 32) {
+        if (norm) QMH_MV(QMH_Q4, 32, true); else QMH_MV(QMH_Q4, 32, false);
+    } else if (a->dtype == QMH_Q8 && a->tile_r == 16) {
+        if (norm) QMH_MV(QMH_Q8, 16, true); else QMH_MV(QMH_Q8, 16, false);
+    } else if (a->dtype == QMH_Q8 && a->tile_r == 32) {
+        if (norm) QMH_MV(QMH_Q8, 32, true); else QMH_MV(QMH_Q8, 32, false);
+    } else {
+        return (int)hipErrorInvalidValue;
+    }
+#undef QMH_MV
+    return (int)hipGetLastError();
+}
+
+extern "C" int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream) {
+    const int grid = (a->rows + QMH_WG - 1) / QMH_WG;
+    hipLaunchKernelGGL(k_matvec_f32, dim3(grid), dim3(QMH_WG), (size_t)a->cols * 4, (hipStream_t)stream, *a);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,313 @@
+// gfx950 small kernels of the quillm token loop: embedding, argmax, and the op-level
+// numerics (fp16, quantization, RMSNorm, softmax, RoPE, SwiGLU, gemm_nt).
+//
+// Rounding contract: bit-identical to the reference's scalar CPU path (built with
+// -ffp-contract=off). The double-precision sums of RMSNorm and softmax are fixed-order tree
+// reductions; the reference sums serially, which can differ in the double's last bits only.
+#include "qmh_device.h"
+#include "qmh_launch.h"
+
+#define QMH_Q8 2
+#define QMH_Q4 3
+
+// ============================================================================ embedding
+
+// x = dequantised row `token` of tok_embd (src/model.c:162 -> src/quant.c:65-101)
+__global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, int vocab, const int32_t *tok_ptr,
+                        float *x) {
+    const int tok = *tok_ptr;
+    if (tok < 0 || tok >= vocab) return;  // stale token in device memory: read nothing
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) {
+        const int b = i >> 5, k = i & 31;
+        float v;
+        if (dtype == QMH_Q8) {
+            const uint8_t *blk = E + ((size_t)tok * ((dim + 31) / 32) + b) * 34;
+            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(int8_t)blk[2 + k];
+        } else if (dtype == QMH_Q4) {
+            const uint8_t *blk = E + ((size_t)tok * ((dim + 31) / 32) + b) * 18;
+            const uint8_t byte = blk[2 + (k >> 1)];
+            const int q = (k & 1) ? (byte >> 4) : (byte & 15);
+            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(q - 8);
+        } else {
+            v = ((const float *)E)[(size_t)tok * dim + i];
+        }
+        x[i] = v;
+    }
+}
+
+extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tok_ptr,
+                                float *x, void *stream) {
+    hipLaunchKernelGGL(k_embed, dim3((dim + 255) / 256), dim3(256), 0, (hipStream_t)stream, tok_embd, dtype, dim,
+                       vocab, tok_ptr, x);
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ argmax
+
+// first index of the maximum (src/sampler.c:27-32): each thread keeps the first strict
+// maximum of its stride, and pairs combine preferring the larger value, then the lower index.
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n, int32_t *out_idx,
+                                                 int32_t *tokpos, int32_t *record, int record_cap) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        if (idx == 0x7fffffff || x[i] > v) {
+            v = x[i];
+            idx = i;
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(v, o);
+        int oi = __shfl_xor(idx, o);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[w] = v;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = blockDim.x >> 6;
+        for (int k = 1; k < nw; k++)
+            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
+                v = bv[k];
+                idx = bi[k];
+            }
+        if (out_idx) *out_idx = idx;
+        if (tokpos) {
+            tokpos[0] = idx;
+            tokpos[1] += 1;
+            const int step = tokpos[2];
+            if (record && step >= 0 && step < record_cap) record[step] = idx;
+            tokpos[2] = step + 1;
+        }
+    }
+}
+
+extern "C" int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record,
+                                 int record_cap, void *stream) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos, record,
+                       record_cap);
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ elementwise
+
+__global__ void k_swiglu(float *gate, const float *up, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float g = gate[i];
+        gate[i] = g / (1.0f + qmh_expf(-g)) * up[i];
+    }
+}
+
+extern "C" int qmh_launch_swiglu(float *gate, const float *up, int64_t n, void *stream) {
+    if (n <= 0) return 0;
+    int64_t grid = (n + 255) / 256;
+    grid = grid > 4096 ? 4096 : grid;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, gate, up, n);
+    return (int)hipGetLastError();
+}
+
+__global__ void k_h2f(const uint16_t *h, float *f, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        f[i] = qmh_h2f(h[i]);
+}
+__global__ void k_f2h(const float *f, uint16_t *h, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        h[i] = qmh_f2h(f[i]);
+}
+
+static unsigned grid_for(int64_t n) {
+    int64_t g = (n + 255) / 256;
+    return (unsigned)(g < 1 ? 1 : (g > 8192 ? 8192 : g));
+}
+
+extern "C" int qmh_launch_h2f(const uint16_t *h, float *f, int64_t n, void *stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_h2f, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, h, f, n);
+    return (int)hipGetLastError();
+}
+extern "C" int qmh_launch_f2h(const float *f, uint16_t *h, int64_t n, void *stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_f2h, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, f, h, n);
+    return (int)hipGetLastError();
+}
+
+// rows x n -> reference-layout Q8_0 / Q4_0 rows (src/quant.c:55-85); 8 lanes per block
+__global__ void k_quantize_rows(const float *__restrict__ x, uint8_t *__restrict__ y, int64_t rows, int64_t n,
+                                int dtype) {
+    const int64_t nb = (n + 31) / 32;
+    const int sub = threadIdx.x & 7;
+    const int64_t gb = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;  // global block id
+    const bool on = gb < rows * nb;
+    const int64_t row = on ? gb / nb : 0, b = on ? gb % nb : 0;
+    float v[4], m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int64_t i = b * 32 + sub * 4 + k;
+        v[k] = (on && i < n) ? x[row * n + i] : 0.0f;
+        const float av = fabsf(v[k]);
+        m = av > m ? av : m;
+    }
+    m = qmh_amax8(m);
+    const float qmax = dtype == QMH_Q4 ? 7.0f : 127.0f;
+    const uint16_t dh = qmh_f2h(m / qmax);
+    const float dd = qmh_h2f(dh);
+    if (!on) return;
+    if (dtype == QMH_Q4) {
+        uint8_t *o = y + (row * nb + b) * 18;
+        if (sub == 0) {
+            o[0] = (uint8_t)(dh & 0xff);
+            o[1] = (uint8_t)(dh >> 8);
+        }
+        for (int j = 0; j < 2; j++) {
+            const int lo = qmh_q4_code(v[2 * j], dd) + 8, hi = qmh_q4_code(v[2 * j + 1], dd) + 8;
+            o[2 + sub * 2 + j] = (uint8_t)(lo | (hi << 4));
+        }
+    } else {
+        uint8_t *o = y + (row * nb + b) * 34;
+        if (sub == 0) {
+            o[0] = (uint8_t)(dh & 0xff);
+            o[1] = (uint8_t)(dh >> 8);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)qmh_q8_code(v[k], dd);
+    }
+}
+
+extern "C" int qmh_launch_quantize_rows(const float *x, uint8_t *y, int64_t rows, int64_t n, int dtype, void *stream) {
+    const int64_t blocks = rows * ((n + 31) / 32);
+    if (blocks <= 0) return 0;
+    const int64_t grid = (blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, x, y, rows, n, dtype);
+    return (int)hipGetLastError();
+}
+
+__global__ void k_row_to_f32(const uint8_t *__restrict__ row, int dtype, float *y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = i >> 5;
+        const int k = (int)(i & 31);
+        if (dtype == QMH_Q8) {
+            const uint8_t *blk = row + b * 34;
+            y[i] = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(int8_t)blk[2 + k];
+        } else if (dtype == QMH_Q4) {
+            const uint8_t *blk = row + b * 18;
+            const uint8_t byte = blk[2 + (k >> 1)];
+            const int q = (k & 1) ? (byte >> 4) : (byte & 15);
+            y[i] = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(q - 8);
+        } else {
+            y[i] = ((const float *)row)[i];
+        }
+    }
+}
+
+extern "C" int qmh_launch_row_to_f32(const uint8_t *row, int dtype, float *y, int64_t n, void *stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_row_to_f32, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, row, dtype, y, n);
+    return (int)hipGetLastError();
+}
+
+// RMSNorm (src/ops.c:93-98): one workgroup; double sum of squares as a fixed tree, then
+// out = (x*inv)*w. The tree sum can differ from the reference's serial double sum in its
+// last bits; the fp32 inv it rounds to is the same unless the two straddle a rounding point.
+__global__ __launch_bounds__(1024) void k_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps) {
+    __shared__ double red[16];
+    double ss = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) ss += (double)x[i] * (double)x[i];
+    ss = qmh_block_sum_d(ss, red);
+    const float inv = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
+}
+
+extern "C" int qmh_launch_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps, void *stream) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, (hipStream_t)stream, out, x, w, n, eps);
+    return (int)hipGetLastError();
+}
+
+// softmax (src/ops.c:100-112), one workgroup
+__global__ __launch_bounds__(1024) void k_softmax(float *x, int64_t n) {
+    __shared__ double red[16];
+    __shared__ float redf[16];
+    float m = -__builtin_inff();
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) m = x[i] > m ? x[i] : m;
+    m = qmh_block_max(m, redf);
+    double sum = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float e = qmh_expf(x[i] - m);
+        x[i] = e;
+        sum += (double)e;
+    }
+    sum = qmh_block_sum_d(sum, red);
+    const float inv = (float)(1.0 / sum);
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) x[i] = x[i] * inv;
+}
+
+extern "C" int qmh_launch_softmax(float *x, int64_t n, void *stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_softmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n);
+    return (int)hipGetLastError();
+}
+
+// RoPE (src/ops.c:114-126) with the (cos, sin) pairs of one position precomputed on the host
+// with the reference's double formula
+__global__ void k_rope(float *v, int64_t n_heads, int64_t hd, const float *cs) {
+    const int64_t npairs = n_heads * (hd / 2);
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < npairs; p += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t h = p / (hd / 2), i = p % (hd / 2);
+        float *e = v + h * hd + 2 * i;
+        const float c = cs[2 * i], s = cs[2 * i + 1], x0 = e[0], x1 = e[1];
+        e[0] = x0 * c - x1 * s;
+        e[1] = x0 * s + x1 * c;
+    }
+}
+
+extern "C" int qmh_launch_rope(float *v, int64_t n_heads, int64_t head_dim, const float *table, int64_t pos,
+                               void *stream) {
+    const int64_t npairs = n_heads * (head_dim / 2);
+    if (npairs <= 0) return 0;
+    hipLaunchKernelGGL(k_rope, dim3(grid_for(npairs)), dim3(256), 0, (hipStream_t)stream, v, n_heads, head_dim,
+                       table + (size_t)pos * (head_dim / 2) * 2);
+    return (int)hipGetLastError();
+}
+
+// gemm_nt in the scalar ISA's order (src/gemm_driver.h:7-28): per element, K is cut into
+// panels of 256 (QM_GEMM_KC, src/kernels.h:37); each panel is a serial fp32 sum from +0 and
+// the panel sums are added to C (from +0) in order. 16x16 outputs per workgroup, panels of A
+// and B staged in LDS (padded rows: conflict-free column walks).
+#define QMH_GEMM_KC 256
+__global__ __launch_bounds__(256) void k_gemm_nt(const float *__restrict__ A, const float *__restrict__ B,
+                                                 float *__restrict__ C, int64_t M, int64_t N, int64_t K) {
+    __shared__ float As[16][QMH_GEMM_KC + 1], Bs[16][QMH_GEMM_KC + 1];
+    const int ty = threadIdx.x / 16, tx = threadIdx.x % 16;
+    const int64_t i = (int64_t)blockIdx.y * 16 + ty, j = (int64_t)blockIdx.x * 16 + tx;
+    float c = 0.0f;
+    for (int64_t k0 = 0; k0 < K; k0 += QMH_GEMM_KC) {
+        const int kc = (int)(K - k0 < QMH_GEMM_KC ? K - k0 : QMH_GEMM_KC);
+        for (int e = threadIdx.x; e < 16 * kc; e += 256) {
+            const int r = e / kc, k = e % kc;
+            const int64_t ai = (int64_t)blockIdx.y * 16 + r, bj = (int64_t)blockIdx.x * 16 + r;
+            As[r][k] = ai < M ? A[ai * K + k0 + k] : 0.0f;
+            Bs[r][k] = bj < N ? B[bj * K + k0 + k] : 0.0f;
+        }
+        __syncthreads();
+        float acc = 0.0f;
+        for (int k = 0; k < kc; k++) acc = acc + As[ty][k] * Bs[tx][k];
+        c = c + acc;
+        __syncthreads();
+    }
+    if (i < M && j < N) C[i * N + j] = c;
+}
+
+extern "C" int qmh_launch_gemm_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
+                                  void *stream) {
+    if (M <= 0 || N <= 0) return 0;
+    dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+    hipLaunchKernelGGL(k_gemm_nt, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);
+    return (int)hipGetLastError();
+}

@@ -49,7 +49,7 @@ const char *qmh_last_error(void) { return g_err; }
 
 /* ------------------------------------------------------------------ runtime */
 
-static int g_ready, g_dev = -1, g_cus = 256;
+static int g_ready, g_dev = -1, g_cus = 256, g_mv_grid = 512;
 static hipStream_t g_stream;
 static float *g_rope_scratch; /* op-level rope: one position's (cos, sin) pairs */
 #define ROPE_SCRATCH_PAIRS 4096
@@ -77,6 +77,9 @@ int qmh_init(int device) {
     HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     HIPCHK(hipMalloc((void **)&g_rope_scratch, sizeof(float) * 2 * ROPE_SCRATCH_PAIRS));
     g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    /* tuning knob: workgroups of the quantized matvec (default 2 per CU) */
+    const char *gv = getenv("QMH_MV_GRID");
+    g_mv_grid = gv && atoi(gv) > 0 ? atoi(gv) : 2 * g_cus;
     g_dev = device;
     g_ready = 1;
     return 0;
@@ -254,7 +257,9 @@ static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *c
         w->rows = total;
         w->ntiles = (int)((total + QMH_TILE_R - 1) / QMH_TILE_R);
     }
-    const size_t slots = (size_t)w->ntiles * (size_t)w->nb * (size_t)w->tile_r;
+    /* + QMH_WEIGHT_PAD_SLOTS: the matvec loads whole chunks unconditionally, so the last chunk
+     * of the last tile may read up to one chunk past the tiles (zeros, never used) */
+    const size_t slots = (size_t)w->ntiles * (size_t)w->nb * (size_t)w->tile_r + QMH_WEIGHT_PAD_SLOTS;
     HIPCHK(hipMalloc(&w->codes, slots * (size_t)cb));
     HIPCHK(hipMalloc((void **)&w->scales, slots * 2));
     HIPCHK(hipMemsetAsync(w->codes, 0, slots * (size_t)cb, g_stream));
@@ -314,7 +319,7 @@ static void mv_args_for(const struct qmh_weight *w, qmh_mv_args *a) {
     a->rows = (int)w->rows;
 }
 
-static int mv_grid_cap(void) { return 2 * g_cus; }
+static int mv_grid_cap(void) { return g_mv_grid; }
 
 static int mv_launch(const qmh_mv_args *a, hipStream_t s) {
     return a->dtype == QMH_F32 ? qmh_launch_matvec_f32(a, s) : qmh_launch_matvec(a, mv_grid_cap(), s);
@@ -348,13 +353,14 @@ struct qmh_model {
     dev_layer *layers;
     struct qmh_weight output;
     float *d_rope;  /* [max_seq][hd/2][2] */
-    float *d_x, *d_xb, *d_q, *d_hb, *d_att, *d_logits, *d_k, *d_vt;
+    float *d_x, *d_xb, *d_q, *d_hb, *d_att, *d_logits, *d_kt, *d_v;
     int32_t *d_tokpos; /* token, pos, step, - */
     int32_t *d_record; /* greedy ids [max_seq] */
     int32_t *h_tokpos; /* pinned [max_seq][4] */
     float *h_logits;   /* pinned [vocab] */
     hipGraph_t graph_fwd, graph_greedy;
     hipGraphExec_t exec_fwd, exec_greedy;
+    int use_graph; /* 0 when QMH_NO_GRAPH is set: the same kernels, enqueued one by one (profiling) */
 };
 
 /* the kernels of one decode step, by stage (which) and layer */
@@ -365,7 +371,7 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq;
     const int32_t *pos_ptr = m->d_tokpos + 1;
     dev_layer *L = &m->layers[l];
-    float *kl = m->d_k + (size_t)l * S_ * m->kvd, *vl = m->d_vt + (size_t)l * S_ * m->kvd;
+    float *kl = m->d_kt + (size_t)l * S_ * m->kvd, *vl = m->d_v + (size_t)l * S_ * m->kvd;
     qmh_mv_args a;
     switch (which) {
     case ST_QKV: /* xb = rmsnorm(x); q,k,v = W xb; rope(q,k); k,v -> cache (src/model.c:166-173) */
@@ -439,6 +445,12 @@ static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
     return 0;
 }
 
+/* one decode step on the library stream: a graph replay, or the same launches one by one */
+static hipError_t run_step(qmh_model *m, int with_argmax) {
+    if (m->use_graph) return hipGraphLaunch(with_argmax ? m->exec_greedy : m->exec_fwd, g_stream);
+    return enqueue_step(m, g_stream, with_argmax) ? hipErrorLaunchFailure : hipSuccess;
+}
+
 /* weight bytes one launch of a stage streams (the algorithmic bytes of the matvecs) */
 static double stage_weight_bytes(const qmh_model *m, int which) {
     const struct qmh_weight *w = which == ST_QKV ? &m->layers[0].qkv
@@ -492,7 +504,7 @@ int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_st
     slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
     hipError_t e = hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream);
     if (e == hipSuccess) e = hipEventRecord(e0, g_stream);
-    for (int32_t k = 0; k < n_steps && e == hipSuccess; k++) e = hipGraphLaunch(m->exec_greedy, g_stream);
+    for (int32_t k = 0; k < n_steps && e == hipSuccess; k++) e = run_step(m, 1);
     if (e == hipSuccess) e = hipEventRecord(e1, g_stream);
     if (e == hipSuccess && out)
         e = hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream);
@@ -543,7 +555,7 @@ void qmh_model_free(qmh_model *m) {
     }
     weight_release(&m->output);
     void *dev[] = {m->d_embd, m->d_norms, m->d_rope, m->d_x,      m->d_xb,     m->d_q, m->d_hb,
-                   m->d_att,  m->d_logits, m->d_k,   m->d_vt, m->d_tokpos, m->d_record};
+                   m->d_att,  m->d_logits, m->d_kt,   m->d_v, m->d_tokpos, m->d_record};
     for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_tokpos) hipHostFree(m->h_tokpos);
@@ -590,8 +602,9 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         if (t[6].dtype != t[8].dtype) return fail("layer %d: w1/w3 must share one dtype", l);
     }
     /* LDS budget of the kernels (64 KiB per workgroup) */
-    const int64_t nbD = (D + 31) / 32, nbH = (H + 31) / 32;
-    if (nbD * (40 + 4 * 2 * QMH_TILE_R) > 65536 || nbH * (40 + 4 * QMH_TILE_R) > 65536 || H > 16384 || D > 16384)
+    const int nbD = (int)((D + 31) / 32), nbH = (int)((H + 31) / 32);
+    if (qmh_matvec_lds_bytes(nbD, 2 * QMH_TILE_R, 1) > 65536 || qmh_matvec_lds_bytes(nbD, QMH_TILE_R, 1) > 65536 ||
+        qmh_matvec_lds_bytes(nbH, QMH_TILE_R, 0) > 65536 || H > 16384 || D > 16384)
         return fail("model dims exceed the kernels' LDS budget");
     if (((int64_t)64 * (m->hd + 1) + (int64_t)m->group * m->hd) * 4 > 65536 || m->group > 15)
         return fail("head_dim/group too large for the attention kernels");
@@ -643,18 +656,21 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMalloc((void **)&m->d_hb, sizeof(float) * 2 * H));
     HIPCHK(hipMalloc((void **)&m->d_att, sizeof(float) * (size_t)c->n_heads * S_));
     HIPCHK(hipMalloc((void **)&m->d_logits, sizeof(float) * V));
-    HIPCHK(hipMalloc((void **)&m->d_k, kv_bytes));
-    HIPCHK(hipMalloc((void **)&m->d_vt, kv_bytes));
+    HIPCHK(hipMalloc((void **)&m->d_kt, kv_bytes));
+    HIPCHK(hipMalloc((void **)&m->d_v, kv_bytes));
     HIPCHK(hipMalloc((void **)&m->d_tokpos, sizeof(int32_t) * 4));
     HIPCHK(hipMalloc((void **)&m->d_record, sizeof(int32_t) * (size_t)S_));
-    HIPCHK(hipMemsetAsync(m->d_k, 0, kv_bytes, g_stream));
-    HIPCHK(hipMemsetAsync(m->d_vt, 0, kv_bytes, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_kt, 0, kv_bytes, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_v, 0, kv_bytes, g_stream));
     HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
     HIPCHK(hipHostMalloc((void **)&m->h_tokpos, sizeof(int32_t) * 4 * (size_t)S_, hipHostMallocDefault));
     HIPCHK(hipHostMalloc((void **)&m->h_logits, sizeof(float) * V, hipHostMallocDefault));
     HIPCHK(hipStreamSynchronize(g_stream));
-    if (capture(m, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
-    if (capture(m, 1, &m->graph_greedy, &m->exec_greedy)) return -1;
+    m->use_graph = getenv("QMH_NO_GRAPH") == NULL;
+    if (m->use_graph && capture(m, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
+    if (m->use_graph && capture(m, 1, &m->graph_greedy, &m->exec_greedy)) return -1;
+    if (!m->use_graph && enqueue_step(m, g_stream, 0)) return -1; /* validate the launches once */
+    HIPCHK(hipStreamSynchronize(g_stream));
     return 0;
 }
 
@@ -733,7 +749,7 @@ float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
     m->h_tokpos[0] = token;
     m->h_tokpos[1] = pos;
     hipError_t e = hipMemcpyAsync(m->d_tokpos, m->h_tokpos, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream);
-    if (e == hipSuccess) e = hipGraphLaunch(m->exec_fwd, g_stream);
+    if (e == hipSuccess) e = run_step(m, 0);
     if (e == hipSuccess)
         e = hipMemcpyAsync(m->h_logits, m->d_logits, sizeof(float) * (size_t)m->cfg.vocab_size, hipMemcpyDeviceToHost,
                            g_stream);
@@ -755,7 +771,7 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
         slot[0] = tokens[i];
         slot[1] = pos0 + i;
         HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream));
-        HIPCHK(hipGraphLaunch(m->exec_fwd, g_stream));
+        HIPCHK(run_step(m, 0));
         if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * V, m->d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, g_stream));
     }
     HIPCHK(hipStreamSynchronize(g_stream));
@@ -769,7 +785,7 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
     int32_t *slot = m->h_tokpos;
     slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
     HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream));
-    for (int32_t k = 0; k < n_steps; k++) HIPCHK(hipGraphLaunch(m->exec_greedy, g_stream));
+    for (int32_t k = 0; k < n_steps; k++) HIPCHK(run_step(m, 1));
     if (n_steps > 0 && out)
         HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
     HIPCHK(hipStreamSynchronize(g_stream));
