@@ -113,16 +113,18 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
     constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
     float acc = 0.0f;
+    // a chunk's V values: unconditional, clamped loads, all in flight together; the next
+    // chunk's are issued before the current chunk's chain runs
+    float vv[LPT];
+#define QMH_PV_LOAD(T0)                                                 \
+    _Pragma("unroll") for (int k = 0; k < LPT; k++) {                   \
+        const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW;      \
+        const int tcl = (T0) + t < n ? (T0) + t : n - 1;                \
+        vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];                 \
+    }
+    QMH_PV_LOAD(0);
     for (int t0 = 0; t0 < n; t0 += QMH_PV_TC) {
         const int nt = min(QMH_PV_TC, n - t0);
-        // the chunk's V values: unconditional, clamped loads, all in flight together
-        float vv[LPT];
-#pragma unroll
-        for (int k = 0; k < LPT; k++) {
-            const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW;
-            const int tcl = t0 + t < n ? t0 + t : n - 1;
-            vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];
-        }
         // probabilities of the chunk, +0 past nt
         for (int e = threadIdx.x; e < group * QMH_PV_TC; e += QMH_WG) {
             const int hl = e / QMH_PV_TC, t = e % QMH_PV_TC;
@@ -135,6 +137,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
             const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW, cc = e % QMH_PV_CW;
             Vs[cc * QMH_PV_VS + t] = t < nt ? vv[k] : 0.0f;
         }
+        if (t0 + QMH_PV_TC < n) QMH_PV_LOAD(t0 + QMH_PV_TC);
         __syncthreads();
         if (chain) {
             // out = out + p_t*v_t in t order; the chunk is zero past nt (p*0 = +0 and the sum,
@@ -152,6 +155,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
         __syncthreads();
     }
     if (chain && i0 + col < hd) out[(size_t)(kvh * group + lane_h) * hd + i0 + col] = acc;
+#undef QMH_PV_LOAD
 }
 
 extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *out, const int32_t *pos_ptr,

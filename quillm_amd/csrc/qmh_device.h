@@ -125,6 +125,23 @@ __device__ __forceinline__ int qmh_q8_code(float v, float dd) {
     r = r > 127.0f ? 127.0f : r;
     return (int)r;
 }
+// qmh_q8_code(v, dd) without a division in the common case. Let q = v/dd (real) and
+// Q = fl(q), the correctly rounded quotient the reference rounds. With rinv = fl(1/dd),
+// r = fl(v*rinv) = q(1+e1)(1+e2), |e1|,|e2| <= 2^-24, and |Q - q| <= |q| 2^-24, so
+// |r - Q| <= 3|q| 2^-24 (+ tiny). |v| <= amax and dd = fp32(fp16(amax/127)) >= (amax/127)/1.5
+// (fp16 subnormal rounding at worst), so |q| <= 190.5 and |r - Q| < 3.5e-5. Hence when r is
+// more than 1e-4 from every rounding boundary k+1/2, rint(r) == rint(Q); otherwise (about 2 in
+// 10^4 values, ties included) the exact division decides.
+__device__ __forceinline__ int qmh_q8_code_fast(float v, float dd, float rinv) {
+    if (dd == 0.0f) return 0;
+    const float r = v * rinv;
+    float k = rintf(r);
+    if (0.5f - fabsf(r - k) < 1e-4f) k = rintf(v / dd);
+    k = k < -127.0f ? -127.0f : k;
+    k = k > 127.0f ? 127.0f : k;
+    return (int)k;
+}
+
 __device__ __forceinline__ int qmh_q4_code(float v, float dd) {
     if (dd == 0.0f) return 0;
     float r = rintf(v / dd);

@@ -120,9 +120,10 @@ __device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *w
         m = qmh_amax8(m);
         const uint16_t dh = qmh_f2h(m / 127.0f);
         const float dd = qmh_h2f(dh);
+        const float rinv = dd != 0.0f ? 1.0f / dd : 0.0f;
         int q[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) q[k] = qmh_q8_code(v[k], dd);
+        for (int k = 0; k < 4; k++) q[k] = qmh_q8_code_fast(v[k], dd, rinv);
         int ps = q[0] + q[1] + q[2] + q[3];
         ps += __shfl_xor(ps, 1);
         ps += __shfl_xor(ps, 2);
@@ -310,11 +311,14 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     uint4 A[CH][NV], B[CH][NV];
     uint32_t As[CH], Bs[CH];
 
+    // lanes past the tile's last block re-read the tile's first block (already in cache)
+    // instead of the next tile, so the unconditional loads add no memory traffic
 #define QMH_LOAD(BUF, BS, TILE, CHK)                                                           \
     {                                                                                          \
-        const size_t base = (size_t)(TILE) * TB + (size_t)(CHK) * CHUNK + tid;                 \
+        const size_t tbase = (size_t)(TILE) * TB;                                              \
         _Pragma("unroll") for (int k = 0; k < CH; k++) {                                       \
-            const size_t slot = base + (size_t)k * QMH_WG;                                     \
+            const int l = (CHK) * CHUNK + k * QMH_WG + tid;                                    \
+            const size_t slot = tbase + (size_t)(l < TB ? l : 0);                              \
             _Pragma("unroll") for (int v = 0; v < NV; v++) BUF[k][v] = codes[slot * NV + v];   \
             BS[k] = a.scales[slot];                                                            \
         }                                                                                      \
@@ -365,8 +369,8 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
             nc = 0;                                                                            \
         }                                                                                      \
         more = nt < a.ntiles;                                                                  \
-        const int row = R == QMH_TILE_R ? tile * R + (tid & (R - 1))                           \
-                                        : tile * (R / 2) + (tid & (R / 2 - 1));                \
+        const int row = R == 2 * QMH_TILE_R ? tile * (R / 2) + (tid & (R / 2 - 1))             \
+                                            : tile * R + (tid & (R - 1));                      \
         EpiIn ein = {0.0f, 1.0f, 0.0f};                                                        \
         if (c == nchunk - 1) ein = epi_fetch(a, row, pos);                                     \
         QMH_LOAD(NXT, NXTS, more ? nt : tile, more ? nc : c);                                  \
@@ -439,17 +443,24 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *strea
     if (lds > 65536 || a->cols > qmh_matvec_max_cols(norm) || a->cols < 1) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
 #define QMH_MV(WT, R, N) hipLaunchKernelGGL((k_matvec<WT, R, N>), dim3(grid), dim3(QMH_WG), lds, s, *a)
-    if (a->dtype == QMH_Q4 && a->tile_r == 16) {
-        if (norm) QMH_MV(QMH_Q4, 16, true); else QMH_MV(QMH_Q4, 16, false);
-    } else if (a->dtype == QMH_Q4 && a->tile_r == 32) {
-        if (norm) QMH_MV(QMH_Q4, 32, true); else QMH_MV(QMH_Q4, 32, false);
-    } else if (a->dtype == QMH_Q8 && a->tile_r == 16) {
-        if (norm) QMH_MV(QMH_Q8, 16, true); else QMH_MV(QMH_Q8, 16, false);
-    } else if (a->dtype == QMH_Q8 && a->tile_r == 32) {
-        if (norm) QMH_MV(QMH_Q8, 32, true); else QMH_MV(QMH_Q8, 32, false);
+#define QMH_MV_R(WT)                                                  \
+    if (a->tile_r == 8) {                                             \
+        if (norm) QMH_MV(WT, 8, true); else QMH_MV(WT, 8, false);     \
+    } else if (a->tile_r == 16) {                                     \
+        if (norm) QMH_MV(WT, 16, true); else QMH_MV(WT, 16, false);   \
+    } else if (a->tile_r == 32) {                                     \
+        if (norm) QMH_MV(WT, 32, true); else QMH_MV(WT, 32, false);   \
+    } else {                                                          \
+        return (int)hipErrorInvalidValue;                             \
+    }
+    if (a->dtype == QMH_Q4) {
+        QMH_MV_R(QMH_Q4);
+    } else if (a->dtype == QMH_Q8) {
+        QMH_MV_R(QMH_Q8);
     } else {
         return (int)hipErrorInvalidValue;
     }
+#undef QMH_MV_R
 #undef QMH_MV
     return (int)hipGetLastError();
 }

@@ -176,8 +176,10 @@ __global__ void k_quantize_rows(const float *__restrict__ x, uint8_t *__restrict
             o[0] = (uint8_t)(dh & 0xff);
             o[1] = (uint8_t)(dh >> 8);
         }
+        // the matvec prologue's division-free path (same codes; pinned here by the op tests)
+        const float rinv = dd != 0.0f ? 1.0f / dd : 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)qmh_q8_code(v[k], dd);
+        for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)qmh_q8_code_fast(v[k], dd, rinv);
     }
 }
 

@@ -77,9 +77,9 @@ int qmh_init(int device) {
     HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     HIPCHK(hipMalloc((void **)&g_rope_scratch, sizeof(float) * 2 * ROPE_SCRATCH_PAIRS));
     g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
-    /* tuning knob: workgroups of the quantized matvec (default 2 per CU) */
+    /* tuning knob: workgroups of the quantized matvec (default 3 per CU: the occupancy its registers allow) */
     const char *gv = getenv("QMH_MV_GRID");
-    g_mv_grid = gv && atoi(gv) > 0 ? atoi(gv) : 2 * g_cus;
+    g_mv_grid = gv && atoi(gv) > 0 ? atoi(gv) : 3 * g_cus;
     g_dev = device;
     g_ready = 1;
     return 0;
@@ -223,10 +223,11 @@ static void weight_release(struct qmh_weight *w) {
 }
 
 /* Build a device weight from nsrc host matrices with the same dtype and cols:
- * interleave = 0: rows appended in order (e.g. [wq; wk; wv]);
- * interleave = 1: two matrices of equal rows, tile t holding 16 rows of each (w1 | w3). */
+ * interleave = 0: rows appended in order (e.g. [wq; wk; wv]), tiles of tile_r (8 or 16) rows;
+ * interleave = 1: two matrices of equal rows, tile t holding 16 rows of each (w1 | w3).
+ * Small matrices get 8-row tiles: twice the workgroups, so more of the GPU streams them. */
 static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *const *src, const int64_t *src_rows,
-                        int64_t cols, int interleave) {
+                        int64_t cols, int interleave, int tile_r) {
     memset(w, 0, sizeof *w);
     w->dtype = dtype;
     w->cols = cols;
@@ -253,7 +254,7 @@ static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *c
         w->rows = src_rows[0];
         w->ntiles = (int)((src_rows[0] + QMH_TILE_R - 1) / QMH_TILE_R);
     } else {
-        w->tile_r = QMH_TILE_R;
+        w->tile_r = tile_r;
         w->rows = total;
         w->ntiles = (int)((total + QMH_TILE_R - 1) / QMH_TILE_R);
     }
@@ -293,7 +294,7 @@ qmh_weight *qmh_weight_upload(int dtype, int64_t rows, int64_t cols, const void 
     if (!w) return NULL;
     const void *src[1] = {host_rows};
     int64_t r[1] = {rows};
-    if (weight_build(w, dtype, 1, src, r, cols, 0)) {
+    if (weight_build(w, dtype, 1, src, r, cols, 0, QMH_TILE_R)) {
         weight_release(w);
         free(w);
         return NULL;
@@ -622,21 +623,21 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         dev_layer *L = &m->layers[l];
         const void *qkv[3] = {t[1].data, t[2].data, t[3].data};
         const int64_t qkv_rows[3] = {D, KV, KV};
-        if (weight_build(&L->qkv, t[1].dtype, 3, qkv, qkv_rows, D, 0)) return -1;
+        if (weight_build(&L->qkv, t[1].dtype, 3, qkv, qkv_rows, D, 0, QMH_TILE_R)) return -1;
         const void *wo[1] = {t[4].data};
         const int64_t wo_rows[1] = {D};
-        if (weight_build(&L->wo, t[4].dtype, 1, wo, wo_rows, D, 0)) return -1;
+        if (weight_build(&L->wo, t[4].dtype, 1, wo, wo_rows, D, 0, 8)) return -1;
         const void *w13[2] = {t[6].data, t[8].data};
         const int64_t w13_rows[2] = {H, H};
-        if (weight_build(&L->w13, t[6].dtype, 2, w13, w13_rows, D, t[6].dtype != QMH_F32)) return -1;
+        if (weight_build(&L->w13, t[6].dtype, 2, w13, w13_rows, D, t[6].dtype != QMH_F32, QMH_TILE_R)) return -1;
         const void *w2[1] = {t[7].data};
         const int64_t w2_rows[1] = {D};
-        if (weight_build(&L->w2, t[7].dtype, 1, w2, w2_rows, H, 0)) return -1;
+        if (weight_build(&L->w2, t[7].dtype, 1, w2, w2_rows, H, 0, 8)) return -1;
     }
     HIPCHK(hipMemcpy(m->d_norms + (size_t)(2 * c->n_layers) * D, norm->data, sizeof(float) * D, hipMemcpyHostToDevice));
     const void *out[1] = {output->data};
     const int64_t out_rows[1] = {V};
-    if (weight_build(&m->output, output->dtype, 1, out, out_rows, D, 0)) return -1;
+    if (weight_build(&m->output, output->dtype, 1, out, out_rows, D, 0, QMH_TILE_R)) return -1;
 
     /* RoPE table for every position, reference formula (src/ops.c:114-126) */
     const size_t pairs = (size_t)S_ * (size_t)(m->hd / 2);

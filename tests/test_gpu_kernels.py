@@ -53,6 +53,35 @@ def test_quantize_rows_bytes(gpu, oracle, dtype):
         assert np.array_equal(dy.to_array(np.uint8).reshape(rows, -1), oracle.quantize(dtype, x)), (rows, n)
 
 
+def test_quantize_q8_rounding_boundaries(gpu, oracle):
+    """The device Q8_0 quantizer rounds v*(1/d) and defers to the exact division near k+1/2:
+    values whose quotient sits on, or a few ulps beside, a half-integer (ties included) and
+    scales down to fp16 subnormals must still give the reference's codes."""
+    rows = []
+    for d_target in (0.3, 0.5, 1.0 / 3.0, 0.0123, 7.7e-6, 2.0 ** -20, 3e-8, 1e-7, 5.5e-8):
+        dd = np.float32(oracle.h2f(oracle.f2h(np.array([d_target], np.float32)))[0])
+        if dd == 0:
+            continue
+        amax = np.float32(127) * dd
+        vals = []
+        for k in range(-127, 127):
+            c = np.float32(k + 0.5) * dd
+            vals += [c, np.nextafter(c, np.float32(np.inf)), np.nextafter(c, np.float32(-np.inf)),
+                     np.nextafter(np.nextafter(c, np.float32(np.inf)), np.float32(np.inf))]
+        vals = np.array(vals, np.float32)
+        vals = vals[np.abs(vals) <= amax]
+        for i in range(0, len(vals), 31):
+            row = np.zeros(32, np.float32)
+            row[0] = amax
+            chunk = vals[i: i + 31]
+            row[1: 1 + len(chunk)] = chunk
+            rows.append(row)
+    x = np.stack(rows)
+    dx, dy = dev(gpu, x), gpu.DeviceBuffer(x.shape[0] * 34)
+    gpu._check(gpu.load_library().qmh_quantize_rows_q8(dx.ptr, dy.ptr, x.shape[0], 32, None), "quantize")
+    assert np.array_equal(dy.to_array(np.uint8).reshape(x.shape[0], -1), oracle.quantize(Q8_0, x))
+
+
 @pytest.mark.parametrize("dtype", [F32, Q8_0, Q4_0])
 def test_row_to_f32(gpu, oracle, dtype):
     n = 1000
