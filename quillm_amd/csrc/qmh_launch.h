@@ -49,8 +49,9 @@ typedef struct {
     int head_dim, max_seq, kvd;
 } qmh_mv_args;
 
+/* nslots: slots the codes/scales allocation holds; slots at or past it are never written */
 int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes, uint16_t *scales,
-                      int tile_r, int64_t row_off, int interleave_half, void *stream);
+                      int tile_r, int64_t row_off, int interleave_half, int64_t nslots, void *stream);
 int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
 /* dynamic LDS bytes the quantized matvec needs (must be <= 64 KiB) */
 size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm);

@@ -21,7 +21,7 @@
 
 __global__ void k_repack(const uint8_t *__restrict__ src, int64_t src_rows, int nb, int bs, int cb,
                          uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int tile_r, int64_t row_off,
-                         int half) {
+                         int half, int64_t nslots) {
     int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= src_rows * nb) return;
     int64_t row = idx / nb;
@@ -38,19 +38,21 @@ __global__ void k_repack(const uint8_t *__restrict__ src, int64_t src_rows, int 
         r = row % hr + (int64_t)half * hr;
     }
     int64_t slot = (tile * nb + b) * tile_r + r;
+    if (slot >= nslots) return;  // the host sized the tiles wrongly: write nothing out of bounds
     scales[slot] = (uint16_t)(blk[0] | (blk[1] << 8));
     uint8_t *dst = codes + slot * cb;
     for (int i = 0; i < cb; i++) dst[i] = blk[2 + i];
 }
 
 extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes,
-                                 uint16_t *scales, int tile_r, int64_t row_off, int interleave_half, void *stream) {
+                                 uint16_t *scales, int tile_r, int64_t row_off, int interleave_half, int64_t nslots,
+                                 void *stream) {
     int bs = dtype == QMH_Q4 ? 18 : 34, cb = dtype == QMH_Q4 ? 16 : 32;
     int64_t total = src_rows * nb;
     if (total <= 0) return 0;
     int64_t grid = (total + 255) / 256;
     hipLaunchKernelGGL(k_repack, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, src, src_rows, nb, bs, cb,
-                       codes, scales, tile_r, row_off, interleave_half);
+                       codes, scales, tile_r, row_off, interleave_half, nslots);
     return (int)hipGetLastError();
 }
 

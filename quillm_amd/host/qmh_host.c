@@ -254,9 +254,10 @@ static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *c
         w->rows = src_rows[0];
         w->ntiles = (int)((src_rows[0] + QMH_TILE_R - 1) / QMH_TILE_R);
     } else {
+        if (tile_r != 8 && tile_r != QMH_TILE_R) return fail("unsupported tile height %d", tile_r);
         w->tile_r = tile_r;
         w->rows = total;
-        w->ntiles = (int)((total + QMH_TILE_R - 1) / QMH_TILE_R);
+        w->ntiles = (int)((total + tile_r - 1) / tile_r);
     }
     /* + QMH_WEIGHT_PAD_SLOTS: the matvec loads whole chunks unconditionally, so the last chunk
      * of the last tile may read up to one chunk past the tiles (zeros, never used) */
@@ -275,7 +276,7 @@ static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *c
         hipError_t e = hipMemcpyAsync(stage, src[i], rb * (size_t)src_rows[i], hipMemcpyHostToDevice, g_stream);
         if (e == hipSuccess)
             e = (hipError_t)qmh_launch_repack(stage, src_rows[i], w->nb, dtype, w->codes, w->scales, w->tile_r,
-                                              row_off, interleave ? i : -1, g_stream);
+                                              row_off, interleave ? i : -1, (int64_t)slots, g_stream);
         if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
         if (e != hipSuccess) rc = fail("weight upload: %s", hipGetErrorString(e));
         row_off += src_rows[i];
