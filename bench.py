@@ -45,6 +45,18 @@ def decode_bytes_per_token(w, positions):
     return weights + kv_read + small, weights
 
 
+def pmc_traffic(name):
+    """HBM bytes per launch of a kernel from its committed counter summary (profiles/NAME), the
+    line `traffic_bytes_per_launch: N` (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel)."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", name)):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(path, w, threads, n_prompt, n_gen, q):
     """The compiled reference (oracle/_ref/ref_driver) on a bounded sample of the workload."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -74,9 +86,12 @@ def main():
     ap.add_argument("--workload", default="c5a")
     ap.add_argument("--prefill", type=int, default=None, help="prompt length (default: the config's 512)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-prompt", type=int, default=8)
-    ap.add_argument("--cpu-gen", type=int, default=24)
+    ap.add_argument("--cpu-prompt", type=int, default=None, help="CPU sample prompt (default: the same P)")
+    ap.add_argument("--cpu-gen", type=int, default=None, help="CPU sample decode steps (default: the same K)")
     ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--probe-copy", action="store_true",
+                    help="first run a known-size streaming kernel (fp16->fp32 of 64 Mi halves: 128 MiB read, "
+                         "256 MiB written) whose FETCH_SIZE/WRITE_SIZE readings calibrate the counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported by this build "
@@ -94,6 +109,15 @@ def main():
     if not q.available():
         raise SystemExit("no gfx950 device visible")
     q.init(0)
+    if args.probe_copy:
+        n = 64 << 20
+        src, dst = q.DeviceBuffer(2 * n), q.DeviceBuffer(4 * n)
+        q._check(q.load_library().qmh_memset(src.ptr, 0x3c, 2 * n), "probe fill")
+        for _ in range(3):
+            q._check(q.load_library().qmh_fp16_to_fp32(src.ptr, dst.ptr, n, None), "probe copy")
+        q.sync()
+        del src, dst
+        log(f"[bench] probe copy: 3 x k_h2f over {n} halves")
 
     # synthetic model file (generated on this host: it does not travel)
     need = 8.5e9 if w.wtype == "q8_0" else 4.5e9
@@ -176,7 +200,8 @@ def main():
         "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
         "roofline": {"kernel": "k_matvec<Q4_0,32> (RMSNorm + W1|W3 + SwiGLU)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic(f"k_matvec_w13_{w.wtype}_{w.name}_pmc.txt") if w.name in ("c5a", "c5b") else None,
                      "bytes_per_launch": int(bytes_w13), "us_per_launch": round(ms_w13 * 1e3, 3)},
         "stages": stages,
         "greedy_ids_head": [int(x) for x in ids[:8]],
@@ -184,8 +209,10 @@ def main():
     }
     if not args.no_cpu:
         cpu_threads = min(os.cpu_count() or 1, 16)
-        log(f"[bench] cpu baseline: reference, {cpu_threads} threads, {args.cpu_prompt}+{args.cpu_gen} tokens")
-        cb = cpu_baseline(path, w, cpu_threads, args.cpu_prompt, args.cpu_gen, q)
+        cp = P if args.cpu_prompt is None else args.cpu_prompt
+        cg = K if args.cpu_gen is None else args.cpu_gen
+        log(f"[bench] cpu baseline: reference, {cpu_threads} threads, {cp}+{cg} tokens")
+        cb = cpu_baseline(path, w, cpu_threads, cp, cg, q)
         if cb is not None:
             out["cpu_baseline"] = {k: v for k, v in cb.items() if k != "tokens"}
     try:

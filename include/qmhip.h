@@ -71,6 +71,11 @@ void qmh_weight_free(qmh_weight *w);
  * quantized blocks are also written there (reference layout). qm_matvec (src/ops.c:57-61)
  * with the per-row dot_f32 / dot_q8 / dot_q4 of src/kernels_scalar.c:6-34. */
 int qmh_matvec(const qmh_weight *W, const float *x, float *y, void *xq, void *stream);
+/* y = W * rmsnorm(x, norm_w, eps) in one launch: the reference's qm_rmsnorm followed by
+ * qm_matvec on its output (src/model.c:165-168,182-183), the fused kernel the model runs.
+ * xq as for qmh_matvec (the quantized normalised activation). */
+int qmh_rmsnorm_matvec(const qmh_weight *W, const float *x, const float *norm_w, float eps, float *y, void *xq,
+                       void *stream);
 
 /* C[M,N] = A[M,K] B[N,K]^T, all row-major contiguous f32. qm_matmul_nt (src/ops.c:81-90) ->
  * gemm_nt (src/gemm_driver.h:7-28), scalar-ISA rounding order (K panels of 256). */
@@ -120,14 +125,16 @@ const qmh_config *qmh_model_config(const qmh_model *m);
  * (src/model.c:158-191). */
 float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos);
 
-/* n tokens at positions pos0..pos0+n-1 in one batched pass. KV cache contents and logits are
- * bitwise those of n sequential qmh_model_forward calls (the reference's prompt loop,
- * src/main.c:127-130). logits: NULL, or host memory for n*vocab floats. 0 or -1. */
+/* n tokens at positions pos0..pos0+n-1, enqueued as one batch with no host round trip between
+ * positions. KV cache contents and logits are bitwise those of n sequential qmh_model_forward
+ * calls (the reference's prompt loop, src/main.c:127-130). logits: NULL, or host memory for
+ * n*vocab floats. 0 or -1. */
 int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits);
 
 /* Greedy decode on the device: n_steps forwards starting with token at pos, each next token
- * the first argmax of the previous logits (reference bench/bench.c:143-149). out[0..n_steps]
- * receives the argmax after each step (n_steps ids). No host round trip between steps. */
+ * the first argmax of the previous logits (reference bench/bench.c:143-149). out[k], k < n_steps,
+ * receives the argmax of the logits of the forward at position pos+k (the token fed at pos+k+1).
+ * No host round trip between steps. */
 int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
 
 /* ------------------------------------------------------------------ measurement

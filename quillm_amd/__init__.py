@@ -75,6 +75,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_weight_upload": (vp, [ctypes.c_int, i64, i64, vp]),
         "qmh_weight_free": (None, [vp]),
         "qmh_matvec": (ctypes.c_int, [vp, vp, vp, vp, vp]),
+        "qmh_rmsnorm_matvec": (ctypes.c_int, [vp, vp, vp, f32, vp, vp, vp]),
         "qmh_matmul_nt": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, vp]),
         "qmh_rmsnorm": (ctypes.c_int, [vp, vp, vp, i64, f32, vp]),
         "qmh_softmax": (ctypes.c_int, [vp, i64, vp]),

@@ -8,9 +8,8 @@
 // element one lane's chain over positions. The caches are laid out for those chains:
 //   K: [kvd][max_seq] per layer (transposed): lanes = positions read consecutive floats;
 //   V: [max_seq][kvd] per layer: a position's row is contiguous.
-// The softmax's double sum is a fixed tree (see qmh_block_sum_d); it can differ from the
-// reference's serial double sum in its last bits, which the fp32 1/sum absorbs unless the
-// two straddle an fp32 rounding boundary.
+// The softmax's double sum is a tree whose float 1/sum is checked against the serial order's
+// error bound (qmh_sum_slack) and recomputed serially when the bound cannot decide it.
 #include "qmh_device.h"
 #include "qmh_launch.h"
 
@@ -102,9 +101,23 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
         double sum = 0.0;
         for (int t = threadIdx.x; t < n; t += QMH_WG) sum += (double)qmh_expf(s[t] - m);
         sum = qmh_block_sum_d(sum, red);
+        const double d = qmh_sum_slack(sum, n);
+        float inv = qmh_recip_of_sum(sum - d);
+        if (inv != qmh_recip_of_sum(sum + d)) {  // uniform: the reference's serial order
+            double ser = 0.0;                    // (P is free until the chunk loop below)
+            for (int t0 = 0; t0 < n; t0 += QMH_PV_TC) {
+                const int nt = min(QMH_PV_TC, n - t0);
+                for (int t = threadIdx.x; t < nt; t += QMH_WG) P[t] = qmh_expf(s[t0 + t] - m);
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    for (int t = 0; t < nt; t++) ser += (double)P[t];
+                __syncthreads();
+            }
+            inv = qmh_recip_of_sum(ser);  // meaningful in thread 0, the only writer below
+        }
         if (threadIdx.x == 0) {
             mx_s[hl] = m;
-            inv_s[hl] = (float)(1.0 / sum);
+            inv_s[hl] = inv;
         }
     }
     __syncthreads();

@@ -103,6 +103,22 @@ __device__ __forceinline__ double qmh_block_sum_d(double v, double *buf) {
     return s;
 }
 
+// The reference sums RMSNorm's squares (src/ops.c:95) and softmax's exponentials
+// (src/ops.c:105-109) serially in double and uses each sum only through a float that is
+// monotone in it: 1/sqrt(ss/n + eps) and 1/sum, each step correctly rounded. Here the sums are
+// trees. Every summation order of n non-negative terms lies within gamma_{n-1}*S of the exact
+// sum S, gamma_k = k*u/(1-k*u), u = 2^-53 (Higham, Accuracy and Stability of Numerical
+// Algorithms, 2nd ed., section 4.2), so the serial sum lies in [s-d, s+d] for a tree's s and
+// d = qmh_sum_slack(s, n) (2*gamma_{n-1}/(1-gamma_{n-1}) plus room for the rounding of d and
+// s+-d). If the float of s-d equals that of s+d, monotonicity makes it the float of the serial
+// sum too; otherwise (a fraction of about n * 7e-9 of the calls) the caller recomputes the sum
+// serially in the reference's order. NaN and infinite sums always take the serial path.
+__device__ __forceinline__ double qmh_sum_slack(double s, int n) { return s * ((double)n * 2.5 + 8.0) * 0x1p-53; }
+__device__ __forceinline__ float qmh_rms_inv(double ss, int n, float eps) {
+    return (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+}
+__device__ __forceinline__ float qmh_recip_of_sum(double s) { return (float)(1.0 / s); }
+
 __device__ __forceinline__ float qmh_block_max(float v, float *buf) {
     v = qmh_wave_max(v);
     const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;

@@ -96,7 +96,17 @@ __device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *w
     float inv = 1.0f;
     if (NORM) {
         ss = qmh_block_sum_d(ss, red);  // its barriers also publish xs/ws
-        inv = (float)(1.0 / sqrt(ss / (double)n + (double)a.eps));
+        const double d = qmh_sum_slack(ss, n32);
+        inv = qmh_rms_inv(ss - d, n, a.eps);
+        if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // same ss in every thread: uniform branch
+            if (threadIdx.x == 0) {
+                double s = 0.0;
+                for (int i = 0; i < n; i++) s += (double)xs[i] * (double)xs[i];
+                red[8] = s;  // red[0..3] hold the tree's partials; 8 is free
+            }
+            __syncthreads();
+            inv = qmh_rms_inv(red[8], n, a.eps);
+        }
     } else {
         __syncthreads();
     }
@@ -421,7 +431,17 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
             ss += v * v;
         }
         ss = qmh_block_sum_d(ss, red);
-        inv = (float)(1.0 / sqrt(ss / (double)n + (double)a.eps));
+        const double d = qmh_sum_slack(ss, n);
+        inv = qmh_rms_inv(ss - d, n, a.eps);
+        if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // uniform; serial sum as the reference
+            if (threadIdx.x == 0) {
+                double s = 0.0;
+                for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
+                red[8] = s;
+            }
+            __syncthreads();
+            inv = qmh_rms_inv(red[8], n, a.eps);
+        }
     }
     for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = a.norm_w ? a.x[i] * inv * a.norm_w[i] : a.x[i];
     __syncthreads();

@@ -2,8 +2,9 @@
 // numerics (fp16, quantization, RMSNorm, softmax, RoPE, SwiGLU, gemm_nt).
 //
 // Rounding contract: bit-identical to the reference's scalar CPU path (built with
-// -ffp-contract=off). The double-precision sums of RMSNorm and softmax are fixed-order tree
-// reductions; the reference sums serially, which can differ in the double's last bits only.
+// -ffp-contract=off). The double-precision sums of RMSNorm and softmax are trees whose float
+// results are checked against the serial order's error bound (qmh_sum_slack), with a serial
+// recomputation when the bound cannot decide them.
 #include "qmh_device.h"
 #include "qmh_launch.h"
 
@@ -44,19 +45,32 @@ extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int
 
 // ============================================================================ argmax
 
-// first index of the maximum (src/sampler.c:27-32): each thread keeps the first strict
-// maximum of its stride, and pairs combine preferring the larger value, then the lower index.
+// first index of the maximum (src/sampler.c:27-32): `if (x[i] > x[best]) best = i` from best = 0,
+// so a NaN at 0 wins and NaNs elsewhere are never chosen. Each thread keeps the first strict
+// maximum of the non-NaN values of its stride (8 loads in flight per round), pairs combine
+// preferring the larger value, then the lower index, and a NaN x[0] overrides the result.
 __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n, int32_t *out_idx,
                                                  int32_t *tokpos, int32_t *record, int record_cap) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     float v = -__builtin_inff();
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += blockDim.x)
-        if (idx == 0x7fffffff || x[i] > v) {
-            v = x[i];
-            idx = i;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
+        float xv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + k * (int)blockDim.x;
+            xv[k] = x[i < n ? i : 0];
         }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + k * (int)blockDim.x;
+            if (i < n && xv[k] == xv[k] && (idx == 0x7fffffff || xv[k] > v)) {
+                v = xv[k];
+                idx = i;
+            }
+        }
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         float ov = __shfl_xor(v, o);
@@ -79,6 +93,7 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, in
                 v = bv[k];
                 idx = bi[k];
             }
+        if (idx == 0x7fffffff || x[0] != x[0]) idx = 0;  // all NaN, or NaN at 0
         if (out_idx) *out_idx = idx;
         if (tokpos) {
             tokpos[0] = idx;
@@ -215,15 +230,24 @@ extern "C" int qmh_launch_row_to_f32(const uint8_t *row, int dtype, float *y, in
     return (int)hipGetLastError();
 }
 
-// RMSNorm (src/ops.c:93-98): one workgroup; double sum of squares as a fixed tree, then
-// out = (x*inv)*w. The tree sum can differ from the reference's serial double sum in its
-// last bits; the fp32 inv it rounds to is the same unless the two straddle a rounding point.
+// RMSNorm (src/ops.c:93-98): one workgroup; double sum of squares as a tree, checked against
+// the serial order's error bound (qmh_sum_slack), then out = (x*inv)*w.
 __global__ __launch_bounds__(1024) void k_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps) {
     __shared__ double red[16];
     double ss = 0.0;
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) ss += (double)x[i] * (double)x[i];
     ss = qmh_block_sum_d(ss, red);
-    const float inv = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+    const double d = qmh_sum_slack(ss, (int)n);
+    float inv = qmh_rms_inv(ss - d, (int)n, eps);
+    if (inv != qmh_rms_inv(ss + d, (int)n, eps)) {  // uniform; serial sum as the reference
+        if (threadIdx.x == 0) {
+            double s = 0.0;
+            for (int64_t i = 0; i < n; i++) s += (double)x[i] * (double)x[i];
+            red[8] = s;
+        }
+        __syncthreads();
+        inv = qmh_rms_inv(red[8], (int)n, eps);
+    }
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
 }
 
@@ -246,7 +270,17 @@ __global__ __launch_bounds__(1024) void k_softmax(float *x, int64_t n) {
         sum += (double)e;
     }
     sum = qmh_block_sum_d(sum, red);
-    const float inv = (float)(1.0 / sum);
+    const double d = qmh_sum_slack(sum, (int)n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
+        if (threadIdx.x == 0) {
+            double s = 0.0;
+            for (int64_t i = 0; i < n; i++) s += (double)x[i];  // this thread's own writes and
+            red[8] = s;                                        // the others', published by the
+        }                                                      // tree sum's barriers
+        __syncthreads();
+        inv = qmh_recip_of_sum(red[8]);
+    }
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) x[i] = x[i] * inv;
 }
 

@@ -340,6 +340,22 @@ int qmh_matvec(const qmh_weight *W, const float *x, float *y, void *xq, void *st
     return 0;
 }
 
+int qmh_rmsnorm_matvec(const qmh_weight *W, const float *x, const float *norm_w, float eps, float *y, void *xq,
+                       void *stream) {
+    if (ensure()) return -1;
+    if (!W || !norm_w) return fail("rmsnorm_matvec: NULL weight or gain");
+    qmh_mv_args a;
+    mv_args_for(W, &a);
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.epi = QMH_EPI_STORE;
+    a.out0 = y;
+    a.xq_out = W->dtype == QMH_F32 ? NULL : (uint8_t *)xq;
+    LCHK(mv_launch(&a, S(stream)));
+    return 0;
+}
+
 /* ------------------------------------------------------------------ model */
 
 typedef struct {

@@ -180,3 +180,86 @@ def test_rope(gpu, oracle, nh, hd, pos):
     dv = dev(gpu, v)
     gpu._check(gpu.load_library().qmh_rope(dv.ptr, nh, hd, pos, 10000.0, None), "rope")
     assert np.array_equal(bits(dv.to_array(np.float32)), bits(oracle.rope(v, nh, hd, pos, 10000.0)))
+
+
+# ---- inputs at a float rounding boundary of the double sums (serial fallback paths)
+
+@pytest.mark.parametrize("n", [64, 288, 4096, 11008])
+def test_rmsnorm_boundary(gpu, oracle, n):
+    from _boundary import rmsnorm_boundary_input
+
+    L = gpu.load_library()
+    for seed in range(6):
+        x = rmsnorm_boundary_input(n, 1e-5, seed)
+        w = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+        dx, dw, do = dev(gpu, x), dev(gpu, w), gpu.DeviceBuffer(n * 4)
+        gpu._check(L.qmh_rmsnorm(do.ptr, dx.ptr, dw.ptr, n, 1e-5, None), "rmsnorm")
+        assert np.array_equal(bits(do.to_array(np.float32)), bits(oracle.rmsnorm(x, w, 1e-5))), (n, seed)
+
+
+@pytest.mark.parametrize("dtype", [F32, Q8_0, Q4_0])
+@pytest.mark.parametrize("n", [64, 288, 4096])
+def test_rmsnorm_matvec_boundary_and_random(gpu, oracle, dtype, n):
+    """The fused RMSNorm prologue of the matvec: boundary inputs (serial fallback) and plain
+    random ones, against rmsnorm then matvec in the oracle."""
+    from _boundary import rmsnorm_boundary_input
+
+    L = gpu.load_library()
+    rows = 200
+    W = (rng.standard_normal((rows, n)) * 0.05).astype(np.float32)
+    Wq = W if dtype == F32 else oracle.quantize(dtype, W)
+    h = L.qmh_weight_upload(dtype, rows, n, np.ascontiguousarray(Wq).ctypes.data)
+    assert h, gpu.last_error()
+    try:
+        for seed in range(4):
+            x = rmsnorm_boundary_input(n, 1e-5, seed) if seed < 3 else rng.standard_normal(n).astype(np.float32)
+            g = (1.0 + 0.1 * np.random.default_rng(seed).standard_normal(n)).astype(np.float32)
+            xn = oracle.rmsnorm(x, g, 1e-5)
+            want, want_xq = oracle.matvec(dtype, Wq, rows, n, xn)
+            dx, dg, dy = dev(gpu, x), dev(gpu, g), gpu.DeviceBuffer(rows * 4)
+            dq = gpu.DeviceBuffer(nblocks(n) * 34)
+            gpu._check(L.qmh_rmsnorm_matvec(h, dx.ptr, dg.ptr, 1e-5, dy.ptr, dq.ptr, None), "rmsnorm_matvec")
+            assert np.array_equal(bits(dy.to_array(np.float32)), bits(want)), (dtype, n, seed)
+            if dtype != F32:
+                assert np.array_equal(dq.to_array(np.uint8), want_xq)
+    finally:
+        L.qmh_weight_free(h)
+
+
+@pytest.mark.parametrize("n", [7, 64, 512, 4096])
+def test_softmax_boundary(gpu, oracle, n):
+    from _boundary import softmax_boundary_input
+
+    L = gpu.load_library()
+    for seed in range(6):
+        s = softmax_boundary_input(n, seed)
+        ds = dev(gpu, s)
+        gpu._check(L.qmh_softmax(ds.ptr, n, None), "softmax")
+        assert np.array_equal(bits(ds.to_array(np.float32)), bits(oracle.softmax(s))), (n, seed)
+
+
+def test_argmax_nan_and_inf_semantics(gpu, oracle):
+    """`if (x[i] > x[best]) best = i` from best = 0: NaN at 0 wins, other NaNs never do."""
+    L = gpu.load_library()
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    cases = [
+        [nan, 1.0, 2.0],
+        [1.0, nan, 2.0, nan],
+        [nan] * 5,
+        [-inf, -inf, -inf],
+        [-inf, nan, -inf, -1.0],
+        [3.0, inf, nan, inf],
+        [0.0, -0.0, 0.0],
+    ]
+    big = np.full(40000, -1.0, np.float32)
+    big[::7] = nan
+    big[12345], big[30001] = 5.0, 5.0
+    cases.append(big)
+    big2 = big.copy()
+    big2[0] = nan
+    cases.append(big2)
+    di = gpu.DeviceBuffer(4)
+    for c in cases:
+        x = np.asarray(c, np.float32)
+        gpu._check(L.qmh_argmax(dev(gpu, x).ptr, x.size, di.ptr, None), "argmax")
+        assert di.to_array(np.int32)[0] == oracle.argmax(x), c[:6]
