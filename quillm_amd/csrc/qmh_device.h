@@ -166,13 +166,29 @@ __device__ __forceinline__ int qmh_q4_code(float v, float dd) {
     return (int)r;
 }
 
+// Reductions over 8 consecutive lanes with DPP (no LDS traffic): lane ^ 1 and lane ^ 2 inside
+// each quad, then the row half-mirror (lane i <-> 7 - i of each 8-lane half row), which pairs
+// every lane with one in the other quad. All 8 lanes end with the group's result.
+template <int CTRL>
+__device__ __forceinline__ int qmh_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+#define QMH_DPP_QXOR1 0xb1      // quad_perm [1,0,3,2]
+#define QMH_DPP_QXOR2 0x4e      // quad_perm [2,3,0,1]
+#define QMH_DPP_HALF_MIRROR 0x141
+
 // amax of a block spread over 8 consecutive lanes (4 values each): NaN never wins, like the
 // reference's `a > amax` scan (src/quant.c:38-42).
 __device__ __forceinline__ float qmh_amax8(float m) {
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-        float p = __shfl_xor(m, o);
-        m = p > m ? p : m;
-    }
-    return m;
+    float p = __int_as_float(qmh_dpp<QMH_DPP_QXOR1>(__float_as_int(m)));
+    m = p > m ? p : m;
+    p = __int_as_float(qmh_dpp<QMH_DPP_QXOR2>(__float_as_int(m)));
+    m = p > m ? p : m;
+    p = __int_as_float(qmh_dpp<QMH_DPP_HALF_MIRROR>(__float_as_int(m)));
+    return p > m ? p : m;
+}
+__device__ __forceinline__ int qmh_sum8(int v) {
+    v += qmh_dpp<QMH_DPP_QXOR1>(v);
+    v += qmh_dpp<QMH_DPP_QXOR2>(v);
+    return v + qmh_dpp<QMH_DPP_HALF_MIRROR>(v);
 }

@@ -23,7 +23,14 @@ enum {
     QMH_EPI_QKV = 2,    /* rows [0,seg1): q with RoPE -> out0; [seg1,seg2): k with RoPE -> K cache
                            row pos (out1); [seg2,rows): v -> transposed V cache column pos (out2) */
     QMH_EPI_SWIGLU = 3, /* interleaved W1|W3 tiles: out0[row] = silu(y1)*y3 (src/ops.c:128-133) */
+    QMH_EPI_SWIGLU_Q = 4, /* as SWIGLU with 64-row tiles (32 outputs = one Q8_0 block), and the block
+                             quantized into the activation image xq_img for the next matvec */
 };
+
+/* Activation image: a vector quantized to Q8_0 in the layout the quantized matvec keeps in LDS,
+ * [codes: nb*32 int8][d: nb fp32 (fp32(fp16(d)))][code sums: nb int32], padded to 16 bytes.
+ * Codes are in element order, or split (even elements then odd) for a Q4_0 consumer. */
+#define QMH_XQ_IMAGE_BYTES(nb) ((((size_t)(nb)) * 40 + 15) & ~(size_t)15)
 
 typedef struct {
     /* weight: tiled codes/scales (quantized) or row-major floats (f32) */
@@ -32,7 +39,7 @@ typedef struct {
     const uint16_t *scales;
     int nb;      /* blocks per row (quantized) */
     int cols;    /* elements per row */
-    int tile_r;  /* rows per tile: QMH_TILE_R, or 2*QMH_TILE_R for interleaved W1|W3 */
+    int tile_r;  /* rows per tile: 8 or 16, or 32 / 64 for interleaved W1|W3 */
     int ntiles;
     int rows;    /* valid output rows (per half for the interleaved W1|W3) */
     /* activation: x[cols]; optional RMSNorm gain (norm_w != NULL) applied before quantization */
@@ -40,6 +47,9 @@ typedef struct {
     const float *norm_w;
     float eps;
     uint8_t *xq_out; /* optional: quantized activation in the reference Q8_0 layout */
+    const void *xq_in; /* instead of x: the activation already quantized, as an image */
+    void *xq_img;      /* SWIGLU_Q: the output image (xq_nb blocks), codes split when xq_split */
+    int xq_nb, xq_split;
     /* epilogue */
     int epi;
     float *out0, *out1, *out2;
@@ -55,6 +65,8 @@ int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, u
 int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
 /* dynamic LDS bytes the quantized matvec needs (must be <= 64 KiB) */
 size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm);
+/* longest row the quantized matvec takes, with (norm = 1) or without the RMSNorm prologue */
+int qmh_matvec_max_cols(int norm);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
 int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
 

@@ -61,10 +61,13 @@ extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, i
 // Every matvec workgroup turns the f32 activation into Q8_0 blocks in its own LDS (the
 // reference quantizes x once per qm_matvec, src/ops.c:59; the result is the same wherever it
 // is computed). With RMSNorm (NORM) the gain is applied first (src/ops.c:93-98), so the
-// normalised vector never round-trips through memory. The activation is read into registers
-// with unconditional, index-clamped loads issued BEFORE the weight loads (the vector-memory
-// counter retires loads in order, so the prologue never waits for weights), then staged in
-// LDS and quantized:
+// normalised vector never round-trips through memory.
+//
+// Thread t holds float4 number k*256 + t of x (and of the gain) for every pass k: the loads are
+// coalesced, issued BEFORE the weight loads (the vector-memory counter retires loads in order,
+// so the prologue never waits for weights), and each thread's float4 is exactly the quarter
+// block it quantizes: block k*32 + t/8, elements 4*(t%8) .. +3. The 8 lanes of a block reduce
+// their amax and code sum with DPP. Results in LDS:
 //   acodes[b*32 + k]: the block's 32 codes. For Q4_0 weights they are stored split, even
 //                     elements in [0,16) and odd elements in [16,32), to match the weight's
 //                     low/high nibbles; asum[b] = sum of the codes.
@@ -72,60 +75,92 @@ extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, i
 
 template <bool NORM>
 struct ActRegs {
-    static constexpr int XR = NORM ? 24 : 48;  // x values per thread: n <= XR*256
-    static constexpr int WR = NORM ? 24 : 1;   // gain values per thread
+    static constexpr int P = NORM ? 6 : 12;  // float4 per thread (passes): cols <= P*1024
 };
 
-template <bool SPLIT, bool NORM>
-__device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *wr, int8_t *acodes, float *ad,
-                           int *asum, double *red, float *stage) {
-    constexpr int XR = ActRegs<NORM>::XR;
-    const int n = a.cols, nb = a.nb, n32 = nb * 32;
-    float *xs = stage, *ws = stage + n32;
-    double ss = 0.0;
+// x (and gain) float4s of the passes that hold blocks; lanes past the end read the last whole
+// float4 (the values are masked later). A row length that is not a multiple of 4 takes scalar loads.
+template <bool NORM>
+__device__ __forceinline__ void act_load(const qmh_mv_args &a, float4 *xr, float4 *wr) {
+    constexpr int P = ActRegs<NORM>::P;
+    const int n = a.cols, tid = threadIdx.x;
+    if ((n & 3) == 0) {
+        const int q_last = (n >> 2) - 1;
+        const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.norm_w;
 #pragma unroll
-    for (int k = 0; k < XR; k++) {
-        const int i = k * QMH_WG + (int)threadIdx.x;
-        if (i < n32) {
-            const float xv = i < n ? xr[k] : 0.0f;
-            xs[i] = xv;
-            if (NORM) ws[i] = i < n ? wr[k] : 0.0f;
-            ss += (double)xv * (double)xv;
-        }
+        for (int k = 0; k < P; k++)
+            if (k * QMH_WG * 4 < n) {
+                const int q = k * QMH_WG + tid, qc = q < q_last ? q : q_last;
+                xr[k] = x4[qc];
+                if (NORM) wr[k] = w4[qc];
+            }
+    } else {
+#pragma unroll
+        for (int k = 0; k < P; k++)
+            if (k * QMH_WG * 4 < n) {
+                float xv[4], wv[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int i = 4 * (k * QMH_WG + tid) + j, ic = i < n ? i : n - 1;
+                    xv[j] = a.x[ic];
+                    wv[j] = NORM ? a.norm_w[ic] : 0.0f;
+                }
+                xr[k] = make_float4(xv[0], xv[1], xv[2], xv[3]);
+                if (NORM) wr[k] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+            }
     }
+}
+
+template <bool SPLIT, bool NORM>
+__device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 *wr, int8_t *acodes, float *ad,
+                           int *asum, double *red) {
+    constexpr int P = ActRegs<NORM>::P;
+    const int n = a.cols, nb = a.nb, tid = threadIdx.x, sub = tid & 7;
     float inv = 1.0f;
     if (NORM) {
-        ss = qmh_block_sum_d(ss, red);  // its barriers also publish xs/ws
-        const double d = qmh_sum_slack(ss, n32);
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < P; k++)
+            if (k * QMH_WG * 4 < n) {
+                const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float xv = 4 * (k * QMH_WG + tid) + j < n ? xa[j] : 0.0f;
+                    ss += (double)xv * (double)xv;
+                }
+            }
+        ss = qmh_block_sum_d(ss, red);
+        const double d = qmh_sum_slack(ss, nb * 32);
         inv = qmh_rms_inv(ss - d, n, a.eps);
         if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // same ss in every thread: uniform branch
-            if (threadIdx.x == 0) {
+            if (tid == 0) {
                 double s = 0.0;
-                for (int i = 0; i < n; i++) s += (double)xs[i] * (double)xs[i];
+                for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
                 red[8] = s;  // red[0..3] hold the tree's partials; 8 is free
             }
             __syncthreads();
             inv = qmh_rms_inv(red[8], n, a.eps);
         }
-    } else {
-        __syncthreads();
     }
-    const int sub = threadIdx.x & 7;
-    const int per_pass = QMH_WG >> 3;
-    for (int b0 = 0; b0 < nb; b0 += per_pass) {
-        const int b = b0 + (threadIdx.x >> 3);
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        if (k * 32 >= nb) break;  // uniform
+        const int b = k * 32 + (tid >> 3), i4 = 4 * (k * QMH_WG + tid);
         const bool on = b < nb;
-        const int i4 = (on ? b : 0) * 32 + sub * 4;
-        const float4 x4 = *(const float4 *)(xs + i4);
-        float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (NORM) w4 = *(const float4 *)(ws + i4);
-        const float xa[4] = {x4.x, x4.y, x4.z, x4.w}, wa[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+        float wa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (NORM) {
+            wa[0] = wr[k].x;
+            wa[1] = wr[k].y;
+            wa[2] = wr[k].z;
+            wa[3] = wr[k].w;
+        }
         float v[4], m = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float xv = (on && i4 + k < n) ? xa[k] : 0.0f;
-            if (NORM) xv = xv * inv * wa[k];  // (x*inv)*w as the reference; 0 stays 0 past n
-            v[k] = xv;
+        for (int j = 0; j < 4; j++) {
+            float xv = (on && i4 + j < n) ? xa[j] : 0.0f;
+            if (NORM) xv = xv * inv * wa[j];  // (x*inv)*w as the reference; 0 stays 0 past n
+            v[j] = xv;
             const float av = fabsf(xv);
             m = av > m ? av : m;
         }
@@ -135,21 +170,16 @@ __device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *w
         const float rinv = dd != 0.0f ? 1.0f / dd : 0.0f;
         int q[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) q[k] = qmh_q8_code_fast(v[k], dd, rinv);
-        int ps = q[0] + q[1] + q[2] + q[3];
-        ps += __shfl_xor(ps, 1);
-        ps += __shfl_xor(ps, 2);
-        ps += __shfl_xor(ps, 4);
+        for (int j = 0; j < 4; j++) q[j] = qmh_q8_code_fast(v[j], dd, rinv);
+        const int ps = qmh_sum8(q[0] + q[1] + q[2] + q[3]);
         if (on) {
             int8_t *c = acodes + b * 32;
             if (SPLIT) {
-                c[sub * 2 + 0] = (int8_t)q[0];
-                c[sub * 2 + 1] = (int8_t)q[2];
-                c[16 + sub * 2 + 0] = (int8_t)q[1];
-                c[16 + sub * 2 + 1] = (int8_t)q[3];
+                *(uint16_t *)(c + sub * 2) = (uint16_t)((q[0] & 0xff) | ((q[2] & 0xff) << 8));
+                *(uint16_t *)(c + 16 + sub * 2) = (uint16_t)((q[1] & 0xff) | ((q[3] & 0xff) << 8));
             } else {
-#pragma unroll
-                for (int k = 0; k < 4; k++) c[sub * 4 + k] = (int8_t)q[k];
+                *(uint32_t *)(c + sub * 4) = (uint32_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) |
+                                                        ((uint32_t)(q[3] & 0xff) << 24));
             }
             if (sub == 0) {
                 ad[b] = dd;
@@ -162,7 +192,7 @@ __device__ void act_finish(const qmh_mv_args &a, const float *xr, const float *w
                     o[1] = (uint8_t)(dh >> 8);
                 }
 #pragma unroll
-                for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)q[k];
+                for (int j = 0; j < 4; j++) o[2 + sub * 4 + j] = (uint8_t)(int8_t)q[j];
             }
         }
     }
@@ -192,9 +222,28 @@ __device__ __forceinline__ EpiIn epi_fetch(const qmh_mv_args &a, int row, int po
     return e;
 }
 
+// Max and sum over the 64 lanes of a wave (all lanes end with the result): DPP inside groups
+// of 8, then lane ^ 8, ^ 16, ^ 32. NaN never wins the max.
+__device__ __forceinline__ float mv_wave_amax(float m) {
+    m = qmh_amax8(m);
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) {
+        const float p = __shfl_xor(m, o);
+        m = p > m ? p : m;
+    }
+    return m;
+}
+__device__ __forceinline__ int mv_wave_sum(int v) {
+    v = qmh_sum8(v);
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
 // y: the row's result. Lanes of one tile hold consecutive rows, so the RoPE partner of row
-// 2i/2i+1 is lane ^ 1 and the W3 partner of an interleaved W1 row is lane + 16.
+// 2i/2i+1 is lane ^ 1 and the W3 partner of an interleaved W1 row is lane + R/2.
 // K goes to a transposed cache [kvd][max_seq], V to a row cache [max_seq][kvd].
+template <int R>
 __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float y, int lane, int pos,
                                             const EpiIn &e) {
     switch (a.epi) {
@@ -219,8 +268,31 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
         break;
     }
     case QMH_EPI_SWIGLU: {  // silu(g)*u (src/ops.c:128-133)
-        const float up = __shfl_down(y, 16);
-        if (lane < 16 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf(-y)) * up;
+        const float up = __shfl_down(y, R / 2);
+        if (lane < R / 2 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf(-y)) * up;
+        break;
+    }
+    case QMH_EPI_SWIGLU_Q: {  // R == 64: lanes 0..31 hold the block (rows 32*b ..), 0 past rows
+        const float up = __shfl_down(y, R / 2);
+        const bool mine = lane < R / 2 && row < a.rows;
+        const float h = mine ? y / (1.0f + qmh_expf(-y)) * up : 0.0f;
+        if (mine && a.out0) a.out0[row] = h;
+        // the next matvec's activation block, as qm_quantize_row_q8 makes it (src/quant.c:55-63)
+        const float m = mv_wave_amax(fabsf(h));
+        const uint16_t dh = qmh_f2h(m / 127.0f);
+        const float dd = qmh_h2f(dh);
+        const int q = qmh_q8_code_fast(h, dd, dd != 0.0f ? 1.0f / dd : 0.0f);
+        const int qs = mv_wave_sum(q);
+        if (lane < R / 2) {
+            const int b = (row - lane) >> 5;
+            uint8_t *img = (uint8_t *)a.xq_img;
+            const int at = a.xq_split ? ((lane & 1) ? 16 + (lane >> 1) : (lane >> 1)) : lane;
+            img[(size_t)b * 32 + at] = (uint8_t)(int8_t)q;
+            if (lane == 0) {
+                ((float *)(img + (size_t)a.xq_nb * 32))[b] = dd;
+                ((int *)(img + (size_t)a.xq_nb * 36))[b] = qs;
+            }
+        }
         break;
     }
     }
@@ -277,45 +349,51 @@ __host__ __device__ __forceinline__ int mv_tstride(int nb) {
     return nb4 + (((4 - nb4) % 64) + 64) % 64;
 }
 
-// dynamic LDS bytes of k_matvec for (nb, R, with RMSNorm prologue or not)
+// dynamic LDS bytes of k_matvec for (nb, R): the activation image (codes, scales, code sums;
+// QMH_XQ_IMAGE_BYTES), then T
 __host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, bool norm) {
-    const size_t t = (size_t)R * mv_tstride(nb), st = (size_t)(norm ? 2 : 1) * nb * 32;
-    return (size_t)nb * 40 + 4 * (t > st ? t : st);
+    (void)norm;
+    return QMH_XQ_IMAGE_BYTES(nb) + 4 * (size_t)R * mv_tstride(nb);
 }
 
-template <int WT, int R, bool NORM>
+// activation modes of k_matvec
+enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
+constexpr int MV_IMAGE_REGS = 4;  // uint4 per thread: images up to 16 KiB (nb <= 409)
+
+template <int WT, int R, int AM>
 __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
+    constexpr bool NORM = AM == MV_ACT_NORM;
     constexpr int CB = WT == QMH_Q4 ? 16 : 32;  // code bytes per block
     constexpr int NV = CB / 16;                 // uint4 per block
     constexpr int CH = WT == QMH_Q4 ? 8 : 4;    // blocks per thread per chunk
     constexpr int CHUNK = QMH_WG * CH;
-    constexpr int XR = ActRegs<NORM>::XR, WR = ActRegs<NORM>::WR;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
 
     const int nb = a.nb, TB = R * nb, nchunk = (TB + CHUNK - 1) / CHUNK, S = mv_tstride(nb);
-    const int tid = threadIdx.x, n = a.cols;
+    const int tid = threadIdx.x;
     int tile = blockIdx.x;
     if (tile >= a.ntiles) return;
 
     int8_t *acodes = (int8_t *)smem;
     float *ad = (float *)(smem + (size_t)nb * 32);
     int *asum = (int *)(smem + (size_t)nb * 36);
-    float *T = (float *)(smem + (size_t)nb * 40);  // [R][S]; first the activation's staging area
+    float *T = (float *)(smem + QMH_XQ_IMAGE_BYTES(nb));  // [R][S] per-block terms
 
-    // 1. activation (and gain) loads, unconditional with clamped indices
-    float xr[XR], wr[WR];
+    // 1. activation (and gain) loads, or the quantized image's
+    float4 xr[AM == MV_ACT_IMAGE ? 1 : ActRegs<NORM>::P], wr[NORM ? ActRegs<NORM>::P : 1];
+    uint4 im[AM == MV_ACT_IMAGE ? MV_IMAGE_REGS : 1];
+    const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
+    if (AM == MV_ACT_IMAGE) {
+        const uint4 *src = (const uint4 *)a.xq_in;
 #pragma unroll
-    for (int k = 0; k < XR; k++) {
-        const int i = k * QMH_WG + tid;
-        xr[k] = a.x[i < n ? i : n - 1];
-    }
-    if (NORM) {
-#pragma unroll
-        for (int k = 0; k < WR; k++) {
-            const int i = k * QMH_WG + tid;
-            wr[k] = a.norm_w[i < n ? i : n - 1];
-        }
+        for (int k = 0; k < MV_IMAGE_REGS; k++)
+            if (k * QMH_WG < nimg) {
+                const int i = k * QMH_WG + tid;
+                im[k] = src[i < nimg ? i : nimg - 1];
+            }
+    } else {
+        act_load<NORM>(a, xr, wr);
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
 
@@ -381,7 +459,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
             nc = 0;                                                                            \
         }                                                                                      \
         more = nt < a.ntiles;                                                                  \
-        const int row = R == 2 * QMH_TILE_R ? tile * (R / 2) + (tid & (R / 2 - 1))             \
+        const int row = R >= 2 * QMH_TILE_R ? tile * (R / 2) + (tid & (R / 2 - 1))             \
                                             : tile * R + (tid & (R - 1));                      \
         EpiIn ein = {0.0f, 1.0f, 0.0f};                                                        \
         if (c == nchunk - 1) ein = epi_fetch(a, row, pos);                                     \
@@ -389,7 +467,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
         QMH_COMPUTE(CUR, CURS, c);                                                             \
         if (c == nchunk - 1) {                                                                 \
             __syncthreads();                                                                   \
-            if (tid < R) mv_epilogue(a, row, mv_chain(T + tid * S, nb), tid, pos, ein);        \
+            if (tid < R) mv_epilogue<R>(a, row, mv_chain(T + tid * S, nb), tid, pos, ein);        \
             __syncthreads();                                                                   \
         }                                                                                      \
         tile = nt;                                                                             \
@@ -398,10 +476,19 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
 
     // 2. first weight chunk, then 3. the activation into LDS while it is in flight
     QMH_LOAD(A, As, tile, 0);
-    act_finish<WT == QMH_Q4, NORM>(a, xr, wr, acodes, ad, asum, red, T);
-    // zero T once: the chain adds whole float4s, the pad past nb must read +0
+    // zero T once (the chain adds whole float4s, the pad past nb must read +0); the
+    // prologue's closing barrier publishes it
     for (int i = tid; i < R * S; i += QMH_WG) T[i] = 0.0f;
-    __syncthreads();
+    if (AM == MV_ACT_IMAGE) {
+#pragma unroll
+        for (int k = 0; k < MV_IMAGE_REGS; k++) {
+            const int i = k * QMH_WG + tid;
+            if (k * QMH_WG < nimg && i < nimg) ((uint4 *)smem)[i] = im[k];
+        }
+        __syncthreads();
+    } else {
+        act_finish<WT == QMH_Q4, NORM>(a, xr, wr, acodes, ad, asum, red);
+    }
 
     int c = 0;
     bool more = true;
@@ -451,29 +538,40 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
     for (int i = 0; i < n; i++) s = s + w[i] * xs[i];
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
     const EpiIn e = epi_fetch(a, row, pos);
-    mv_epilogue(a, row, s, threadIdx.x & 15, pos, e);
+    mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e);
 }
 
 extern "C" size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm) { return mv_lds_bytes(nb, tile_r, norm != 0); }
 
-extern "C" int qmh_matvec_max_cols(int norm) { return ActRegs<true>::XR * QMH_WG * (norm ? 1 : 2); }
+extern "C" int qmh_matvec_max_cols(int norm) { return (norm ? ActRegs<true>::P : ActRegs<false>::P) * QMH_WG * 4; }
 
 extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream) {
     const int grid = a->ntiles < grid_cap ? a->ntiles : grid_cap;
-    const bool norm = a->norm_w != NULL;
+    const bool norm = a->norm_w != NULL, image = a->xq_in != NULL;
     const size_t lds = mv_lds_bytes(a->nb, a->tile_r, norm);
-    if (lds > 65536 || a->cols > qmh_matvec_max_cols(norm) || a->cols < 1) return (int)hipErrorInvalidValue;
+    if (lds > 65536 || a->cols > qmh_matvec_max_cols(norm) || a->cols < 1 || (norm && image)) return (int)hipErrorInvalidValue;
+    if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)MV_IMAGE_REGS * QMH_WG * 16) return (int)hipErrorInvalidValue;
+    if ((a->epi == QMH_EPI_SWIGLU_Q) != (a->tile_r == 64)) return (int)hipErrorInvalidValue;
+    const int am = image ? MV_ACT_IMAGE : norm ? MV_ACT_NORM : MV_ACT;
     hipStream_t s = (hipStream_t)stream;
-#define QMH_MV(WT, R, N) hipLaunchKernelGGL((k_matvec<WT, R, N>), dim3(grid), dim3(QMH_WG), lds, s, *a)
-#define QMH_MV_R(WT)                                                  \
-    if (a->tile_r == 8) {                                             \
-        if (norm) QMH_MV(WT, 8, true); else QMH_MV(WT, 8, false);     \
-    } else if (a->tile_r == 16) {                                     \
-        if (norm) QMH_MV(WT, 16, true); else QMH_MV(WT, 16, false);   \
-    } else if (a->tile_r == 32) {                                     \
-        if (norm) QMH_MV(WT, 32, true); else QMH_MV(WT, 32, false);   \
-    } else {                                                          \
-        return (int)hipErrorInvalidValue;                             \
+#define QMH_MV(WT, R, AM) hipLaunchKernelGGL((k_matvec<WT, R, AM>), dim3(grid), dim3(QMH_WG), lds, s, *a)
+#define QMH_MV_R(WT)                                                                    \
+    if (a->tile_r == 8 || a->tile_r == 16) {                                            \
+        if (am == MV_ACT_NORM) {                                                        \
+            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT_NORM); else QMH_MV(WT, 16, MV_ACT_NORM); \
+        } else if (am == MV_ACT_IMAGE) {                                                \
+            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT_IMAGE); else QMH_MV(WT, 16, MV_ACT_IMAGE); \
+        } else {                                                                        \
+            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT); else QMH_MV(WT, 16, MV_ACT);     \
+        }                                                                               \
+    } else if (a->tile_r == 32) {                                                       \
+        if (am == MV_ACT_NORM) QMH_MV(WT, 32, MV_ACT_NORM); else if (am == MV_ACT) QMH_MV(WT, 32, MV_ACT); \
+        else return (int)hipErrorInvalidValue;                                          \
+    } else if (a->tile_r == 64) {                                                       \
+        if (am == MV_ACT_NORM) QMH_MV(WT, 64, MV_ACT_NORM); else if (am == MV_ACT) QMH_MV(WT, 64, MV_ACT); \
+        else return (int)hipErrorInvalidValue;                                          \
+    } else {                                                                            \
+        return (int)hipErrorInvalidValue;                                               \
     }
     if (a->dtype == QMH_Q4) {
         QMH_MV_R(QMH_Q4);

@@ -224,8 +224,9 @@ static void weight_release(struct qmh_weight *w) {
 
 /* Build a device weight from nsrc host matrices with the same dtype and cols:
  * interleave = 0: rows appended in order (e.g. [wq; wk; wv]), tiles of tile_r (8 or 16) rows;
- * interleave = 1: two matrices of equal rows, tile t holding 16 rows of each (w1 | w3).
- * Small matrices get 8-row tiles: twice the workgroups, so more of the GPU streams them. */
+ * interleave = 1: two matrices of equal rows, tile t holding tile_r/2 rows of each (w1 | w3;
+ * tile_r 32 or 64). Small matrices get 8-row tiles: twice the workgroups, so more of the GPU
+ * streams them. */
 static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *const *src, const int64_t *src_rows,
                         int64_t cols, int interleave, int tile_r) {
     memset(w, 0, sizeof *w);
@@ -250,9 +251,10 @@ static int weight_build(struct qmh_weight *w, int dtype, int nsrc, const void *c
     const size_t rb = qlm_row_bytes(dtype, cols);
     if (interleave) {
         if (nsrc != 2 || src_rows[0] != src_rows[1]) return fail("interleaved weight needs two equal matrices");
-        w->tile_r = 2 * QMH_TILE_R;
+        if (tile_r != 32 && tile_r != 64) return fail("unsupported interleaved tile height %d", tile_r);
+        w->tile_r = tile_r;
         w->rows = src_rows[0];
-        w->ntiles = (int)((src_rows[0] + QMH_TILE_R - 1) / QMH_TILE_R);
+        w->ntiles = (int)((src_rows[0] + tile_r / 2 - 1) / (tile_r / 2));
     } else {
         if (tile_r != 8 && tile_r != QMH_TILE_R) return fail("unsupported tile height %d", tile_r);
         w->tile_r = tile_r;
@@ -360,6 +362,7 @@ int qmh_rmsnorm_matvec(const qmh_weight *W, const float *x, const float *norm_w,
 
 typedef struct {
     struct qmh_weight qkv, wo, w13, w2;
+    int w2_image; /* W1|W3 and W2 quantized: W13 writes W2's input as a quantized image (d_hq) */
 } dev_layer;
 
 struct qmh_model {
@@ -372,6 +375,7 @@ struct qmh_model {
     struct qmh_weight output;
     float *d_rope;  /* [max_seq][hd/2][2] */
     float *d_x, *d_xb, *d_q, *d_hb, *d_att, *d_logits, *d_kt, *d_v;
+    void *d_hq; /* W2's input quantized (QMH_XQ_IMAGE_BYTES(nb of hidden_dim)) */
     int32_t *d_tokpos; /* token, pos, step, - */
     int32_t *d_record; /* greedy ids [max_seq] */
     int32_t *h_tokpos; /* pinned [max_seq][4] */
@@ -432,10 +436,21 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
             return rc ? rc : qmh_launch_swiglu(m->d_hb, m->d_hb + H, H, s);
         }
         a.epi = QMH_EPI_SWIGLU;
+        if (L->w2_image) { /* hb goes straight to W2's quantized input (src/ops.c:59 on hb) */
+            a.epi = QMH_EPI_SWIGLU_Q;
+            a.out0 = NULL;
+            a.xq_img = m->d_hq;
+            a.xq_nb = (H + 31) / 32;
+            a.xq_split = L->w2.dtype == QMH_Q4_0;
+        }
         return mv_launch(&a, s);
     case ST_W2: /* x += W2 hb (src/model.c:185-186) */
         mv_args_for(&L->w2, &a);
         a.x = m->d_hb;
+        if (L->w2_image) {
+            a.x = NULL;
+            a.xq_in = m->d_hq;
+        }
         a.epi = QMH_EPI_ADD;
         a.out0 = m->d_x;
         return mv_launch(&a, s);
@@ -572,8 +587,8 @@ void qmh_model_free(qmh_model *m) {
         free(m->layers);
     }
     weight_release(&m->output);
-    void *dev[] = {m->d_embd, m->d_norms, m->d_rope, m->d_x,      m->d_xb,     m->d_q, m->d_hb,
-                   m->d_att,  m->d_logits, m->d_kt,   m->d_v, m->d_tokpos, m->d_record};
+    void *dev[] = {m->d_embd, m->d_norms, m->d_rope, m->d_x,      m->d_xb,     m->d_q,      m->d_hb,
+                   m->d_hq,   m->d_att,   m->d_logits, m->d_kt,  m->d_v, m->d_tokpos, m->d_record};
     for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_tokpos) hipHostFree(m->h_tokpos);
@@ -621,9 +636,10 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     }
     /* LDS budget of the kernels (64 KiB per workgroup) */
     const int nbD = (int)((D + 31) / 32), nbH = (int)((H + 31) / 32);
-    if (qmh_matvec_lds_bytes(nbD, 2 * QMH_TILE_R, 1) > 65536 || qmh_matvec_lds_bytes(nbD, QMH_TILE_R, 1) > 65536 ||
-        qmh_matvec_lds_bytes(nbH, QMH_TILE_R, 0) > 65536 || H > 16384 || D > 16384)
-        return fail("model dims exceed the kernels' LDS budget");
+    if (qmh_matvec_lds_bytes(nbD, 64, 1) > 65536 || qmh_matvec_lds_bytes(nbD, QMH_TILE_R, 1) > 65536 ||
+        qmh_matvec_lds_bytes(nbH, QMH_TILE_R, 0) > 65536 || D > qmh_matvec_max_cols(1) || H > qmh_matvec_max_cols(0))
+        return fail("model dims exceed the kernels' limits (dim <= %d, hidden_dim <= %d)", qmh_matvec_max_cols(1),
+                    qmh_matvec_max_cols(0));
     if (((int64_t)64 * (m->hd + 1) + (int64_t)m->group * m->hd) * 4 > 65536 || m->group > 15)
         return fail("head_dim/group too large for the attention kernels");
 
@@ -646,7 +662,9 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         if (weight_build(&L->wo, t[4].dtype, 1, wo, wo_rows, D, 0, 8)) return -1;
         const void *w13[2] = {t[6].data, t[8].data};
         const int64_t w13_rows[2] = {H, H};
-        if (weight_build(&L->w13, t[6].dtype, 2, w13, w13_rows, D, t[6].dtype != QMH_F32, QMH_TILE_R)) return -1;
+        L->w2_image = t[6].dtype != QMH_F32 && t[7].dtype != QMH_F32;
+        if (weight_build(&L->w13, t[6].dtype, 2, w13, w13_rows, D, t[6].dtype != QMH_F32, L->w2_image ? 64 : 32))
+            return -1;
         const void *w2[1] = {t[7].data};
         const int64_t w2_rows[1] = {D};
         if (weight_build(&L->w2, t[7].dtype, 1, w2, w2_rows, H, 0, 8)) return -1;
@@ -672,6 +690,8 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMalloc((void **)&m->d_xb, sizeof(float) * D));
     HIPCHK(hipMalloc((void **)&m->d_q, sizeof(float) * D));
     HIPCHK(hipMalloc((void **)&m->d_hb, sizeof(float) * 2 * H));
+    HIPCHK(hipMalloc(&m->d_hq, QMH_XQ_IMAGE_BYTES((H + 31) / 32)));
+    HIPCHK(hipMemsetAsync(m->d_hq, 0, QMH_XQ_IMAGE_BYTES((H + 31) / 32), g_stream)); /* the pad reads as 0 */
     HIPCHK(hipMalloc((void **)&m->d_att, sizeof(float) * (size_t)c->n_heads * S_));
     HIPCHK(hipMalloc((void **)&m->d_logits, sizeof(float) * V));
     HIPCHK(hipMalloc((void **)&m->d_kt, kv_bytes));
