@@ -2,7 +2,8 @@
 //
 // Everything here reproduces the reference's scalar CPU arithmetic bit for bit. The file is
 // compiled with -ffp-contract=off, so a*b+c is two roundings, as in the reference (ISO C
-// mode, no FMA); the only fused multiply-adds are the explicit fma() calls in qmh_expf.
+// mode, no FMA); the only fused multiply-adds are the explicit fma() calls of qmh_expf and
+// qmh_div127, parts of exact algorithms.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -15,24 +16,35 @@
 // (fp16 denormals are on by default on gfx9); reference src/fp16.c:6-31.
 __device__ __forceinline__ float qmh_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
-// float -> fp16 bits, round to nearest even, as reference src/fp16.c:33-56 for the values the
-// quantizer produces (non-negative scales; NaN kept quiet with its top payload bits).
-// Integer-only so the result does not depend on the MODE register.
+// float -> fp16 bits, round to nearest even, as reference src/fp16.c:33-56 (NaN kept quiet with
+// its top payload bits). Integer-only so the result does not depend on the MODE register, and
+// branch-free: every case is computed and selected.
 __device__ __forceinline__ uint16_t qmh_f2h(float f) {
-    uint32_t u = __float_as_uint(f);
-    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
-    int e = (int)(a >> 23) - 127;                        // unbiased exponent
-    if (e >= 16) return (uint16_t)(sign | 0x7c00u);       // 2^16 and up (and inf) -> inf
-    if (e < -25) return (uint16_t)sign;                   // below 2^-25 -> signed zero
-    uint32_t mant = (a & 0x7fffffu) | 0x800000u;
-    int sh = e >= -14 ? 13 : 13 + (-14 - e);              // 13 (normal) .. 24 (deep subnormal)
-    uint32_t q = mant >> sh, rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    const int e = (int)(a >> 23) - 127;                   // unbiased exponent
+    const uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+    int sh = e >= -14 ? 13 : 13 + (-14 - e);              // 13 (normal) .. subnormal shifts
+    sh = sh < 25 ? sh : 25;                               // below 2^-25 everything rounds to 0
+    uint32_t q = mant >> sh;
+    const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
     q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
     // a normal q carries the implicit bit, so adding the biased exponent minus one both
     // places it and lets a rounding carry roll into the exponent (65520 -> inf)
     uint32_t r = e >= -14 ? (((uint32_t)(e + 14) << 10) + q) : q;
+    r = e >= 16 ? 0x7c00u : r;                            // 2^16 and up (and inf) -> inf
+    r = a > 0x7f800000u ? (0x7e00u | ((a >> 13) & 0x3ffu)) : r;
     return (uint16_t)(sign | r);
+}
+
+// m / 127.0f for m >= 0, correctly rounded without a division: q0 = m * fl(1/127), one FMA for
+// the exact residual m - 127*q0 and one to correct q0. Checked equal to the IEEE quotient for
+// every non-negative float except +inf, which is selected explicitly.
+__device__ __forceinline__ float qmh_div127(float m) {
+    const float r = 1.0f / 127.0f;
+    const float q0 = m * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, m), r, q0);
+    return m == __builtin_inff() ? m : q1;
 }
 
 // expf exactly as the host's glibc computes it (glibc >= 2.27 uses the ARM optimized-routines
@@ -84,9 +96,28 @@ __device__ __forceinline__ float qmh_wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
 }
+template <int CTRL>
+__device__ __forceinline__ int qmh_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+#define QMH_DPP_QXOR1 0xb1      // quad_perm [1,0,3,2]
+#define QMH_DPP_QXOR2 0x4e      // quad_perm [2,3,0,1]
+#define QMH_DPP_HALF_MIRROR 0x141
+#define QMH_DPP_MIRROR 0x140
+template <int CTRL>
+__device__ __forceinline__ double qmh_dpp_d(double v) {
+    const int lo = qmh_dpp<CTRL>(__double2loint(v)), hi = qmh_dpp<CTRL>(__double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+// sum over the 64 lanes (fixed order; all lanes get it): DPP within quads, 8- and 16-lane rows
+// (the half-mirror / mirror pair each lane with one in the other half), then lane ^ 16, ^ 32
 __device__ __forceinline__ double qmh_wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v += qmh_dpp_d<QMH_DPP_QXOR1>(v);
+    v += qmh_dpp_d<QMH_DPP_QXOR2>(v);
+    v += qmh_dpp_d<QMH_DPP_HALF_MIRROR>(v);
+    v += qmh_dpp_d<QMH_DPP_MIRROR>(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
     return v;
 }
 
@@ -142,12 +173,14 @@ __device__ __forceinline__ int qmh_q8_code(float v, float dd) {
     return (int)r;
 }
 // qmh_q8_code(v, dd) without a division in the common case. Let q = v/dd (real) and
-// Q = fl(q), the correctly rounded quotient the reference rounds. With rinv = fl(1/dd),
-// r = fl(v*rinv) = q(1+e1)(1+e2), |e1|,|e2| <= 2^-24, and |Q - q| <= |q| 2^-24, so
-// |r - Q| <= 3|q| 2^-24 (+ tiny). |v| <= amax and dd = fp32(fp16(amax/127)) >= (amax/127)/1.5
-// (fp16 subnormal rounding at worst), so |q| <= 190.5 and |r - Q| < 3.5e-5. Hence when r is
-// more than 1e-4 from every rounding boundary k+1/2, rint(r) == rint(Q); otherwise (about 2 in
-// 10^4 values, ties included) the exact division decides.
+// Q = fl(q), the correctly rounded quotient the reference rounds. rinv approximates 1/dd with
+// relative error at most 2^-22 (the hardware reciprocal is specified to 1 ulp), so
+// r = fl(v*rinv) = q(1+e1)(1+e2), |e1| <= 2^-22, |e2| <= 2^-24, and |Q - q| <= |q| 2^-24, giving
+// |r - Q| <= |q| (2^-22 + 2^-23) (+ tiny). |v| <= amax and dd = fp32(fp16(amax/127)) >=
+// (amax/127)/1.5 (fp16 subnormal rounding at worst), so |q| <= 190.5 and |r - Q| < 7e-5.
+// Hence when r is more than 1e-4 from every rounding boundary k+1/2, rint(r) == rint(Q);
+// otherwise (about 2 in 10^4 values, ties included) the exact division decides.
+__device__ __forceinline__ float qmh_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ int qmh_q8_code_fast(float v, float dd, float rinv) {
     if (dd == 0.0f) return 0;
     const float r = v * rinv;
@@ -156,6 +189,30 @@ __device__ __forceinline__ int qmh_q8_code_fast(float v, float dd, float rinv) {
     k = k < -127.0f ? -127.0f : k;
     k = k > 127.0f ? 127.0f : k;
     return (int)k;
+}
+// the same for the 4 values of a lane, with one branch to the exact division for all of them
+__device__ __forceinline__ void qmh_q8_codes4(const float *v, float dd, float rinv, int *q) {
+    float k[4];
+    bool slow = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float r = v[j] * rinv;
+        k[j] = rintf(r);
+        slow |= 0.5f - fabsf(r - k[j]) < 1e-4f;
+    }
+    if (slow) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float r = v[j] * rinv;
+            if (0.5f - fabsf(r - rintf(r)) < 1e-4f) k[j] = rintf(v[j] / dd);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float c = k[j] < -127.0f ? -127.0f : k[j];
+        c = c > 127.0f ? 127.0f : c;
+        q[j] = dd == 0.0f ? 0 : (int)c;
+    }
 }
 
 __device__ __forceinline__ int qmh_q4_code(float v, float dd) {
@@ -169,14 +226,6 @@ __device__ __forceinline__ int qmh_q4_code(float v, float dd) {
 // Reductions over 8 consecutive lanes with DPP (no LDS traffic): lane ^ 1 and lane ^ 2 inside
 // each quad, then the row half-mirror (lane i <-> 7 - i of each 8-lane half row), which pairs
 // every lane with one in the other quad. All 8 lanes end with the group's result.
-template <int CTRL>
-__device__ __forceinline__ int qmh_dpp(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
-}
-#define QMH_DPP_QXOR1 0xb1      // quad_perm [1,0,3,2]
-#define QMH_DPP_QXOR2 0x4e      // quad_perm [2,3,0,1]
-#define QMH_DPP_HALF_MIRROR 0x141
-
 // amax of a block spread over 8 consecutive lanes (4 values each): NaN never wins, like the
 // reference's `a > amax` scan (src/quant.c:38-42).
 __device__ __forceinline__ float qmh_amax8(float m) {

@@ -165,12 +165,10 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
             m = av > m ? av : m;
         }
         m = qmh_amax8(m);
-        const uint16_t dh = qmh_f2h(m / 127.0f);
+        const uint16_t dh = qmh_f2h(qmh_div127(m));
         const float dd = qmh_h2f(dh);
-        const float rinv = dd != 0.0f ? 1.0f / dd : 0.0f;
         int q[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) q[j] = qmh_q8_code_fast(v[j], dd, rinv);
+        qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
         const int ps = qmh_sum8(q[0] + q[1] + q[2] + q[3]);
         if (on) {
             int8_t *c = acodes + b * 32;
@@ -279,9 +277,9 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
         if (mine && a.out0) a.out0[row] = h;
         // the next matvec's activation block, as qm_quantize_row_q8 makes it (src/quant.c:55-63)
         const float m = mv_wave_amax(fabsf(h));
-        const uint16_t dh = qmh_f2h(m / 127.0f);
+        const uint16_t dh = qmh_f2h(qmh_div127(m));
         const float dd = qmh_h2f(dh);
-        const int q = qmh_q8_code_fast(h, dd, dd != 0.0f ? 1.0f / dd : 0.0f);
+        const int q = qmh_q8_code_fast(h, dd, qmh_rcp(dd));
         const int qs = mv_wave_sum(q);
         if (lane < R / 2) {
             const int b = (row - lane) >> 5;
@@ -298,29 +296,29 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
     }
 }
 
-// The serial chain of one row: s = +0; s = s + t[b] for b = 0..nb-1, reading the row as
-// float4s with the next 8 float4s in flight while the current 32 terms are added. The row is
-// zero past nb (adding +0 to a sum that started at +0 changes nothing: such a sum is never
-// -0) and reads stay inside the row's LDS stride.
+// The serial chain of one row: s = +0; s = s + t[b] for b = 0..nb-1. The row is read as
+// chunks of 32 floats (8 float4) with the next chunk in flight while the current one is added;
+// rows are zero from nb to a whole chunk (adding +0 to a sum that started at +0 changes
+// nothing: such a sum is never -0), so the loop has no conditions.
 __device__ __forceinline__ float mv_chain(const float *row, int nb) {
     const float4 *r4 = (const float4 *)row;
-    const int n4 = (nb + 3) >> 2;
+    const int nc = (nb + 31) >> 5;
     float s = 0.0f;
     float4 v[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) v[k] = r4[k < n4 ? k : 0];
-    for (int k0 = 0; k0 < n4; k0 += 8) {
+    for (int k = 0; k < 8; k++) v[k] = r4[k];
+    for (int c = 0; c < nc; c++) {
+        const int nx = c + 1 < nc ? c + 1 : c;
         float4 w[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) w[k] = r4[k0 + 8 + k < n4 ? k0 + 8 + k : 0];
+        for (int k = 0; k < 8; k++) w[k] = r4[nx * 8 + k];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            if (k0 + k < n4) {
-                s = s + v[k].x;
-                s = s + v[k].y;
-                s = s + v[k].z;
-                s = s + v[k].w;
-            }
+        for (int k = 0; k < 8; k++) {
+            s = s + v[k].x;
+            s = s + v[k].y;
+            s = s + v[k].z;
+            s = s + v[k].w;
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) v[k] = w[k];
     }
@@ -342,11 +340,12 @@ __device__ __forceinline__ float mv_chain(const float *row, int nb) {
 //   3. after the tile's last chunk, lanes 0..R-1 run each row's serial chain, then the
 //      epilogue.
 
-// LDS row stride of T: >= nb rounded up to 4, and == 4 mod 64 floats so the chain lanes'
-// float4 reads and the compute phase's writes fall in distinct banks
+// LDS row stride of T: >= nb rounded up to whole 32-float chunks (the chain reads them), and
+// == 4 mod 64 floats so the chain lanes' float4 reads and the compute phase's writes fall in
+// distinct banks
 __host__ __device__ __forceinline__ int mv_tstride(int nb) {
-    const int nb4 = (nb + 3) & ~3;
-    return nb4 + (((4 - nb4) % 64) + 64) % 64;
+    const int n32 = (nb + 31) & ~31;
+    return n32 + (((4 - n32) % 64) + 64) % 64;
 }
 
 // dynamic LDS bytes of k_matvec for (nb, R): the activation image (codes, scales, code sums;

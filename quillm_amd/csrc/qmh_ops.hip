@@ -171,8 +171,7 @@ __global__ void k_quantize_rows(const float *__restrict__ x, uint8_t *__restrict
         m = av > m ? av : m;
     }
     m = qmh_amax8(m);
-    const float qmax = dtype == QMH_Q4 ? 7.0f : 127.0f;
-    const uint16_t dh = qmh_f2h(m / qmax);
+    const uint16_t dh = qmh_f2h(dtype == QMH_Q4 ? m / 7.0f : qmh_div127(m));
     const float dd = qmh_h2f(dh);
     if (!on) return;
     if (dtype == QMH_Q4) {
@@ -192,9 +191,10 @@ __global__ void k_quantize_rows(const float *__restrict__ x, uint8_t *__restrict
             o[1] = (uint8_t)(dh >> 8);
         }
         // the matvec prologue's division-free path (same codes; pinned here by the op tests)
-        const float rinv = dd != 0.0f ? 1.0f / dd : 0.0f;
+        int q[4];
+        qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
 #pragma unroll
-        for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)qmh_q8_code_fast(v[k], dd, rinv);
+        for (int k = 0; k < 4; k++) o[2 + sub * 4 + k] = (uint8_t)(int8_t)q[k];
     }
 }
 
