@@ -98,6 +98,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
         float m = -__builtin_inff();
         for (int t = threadIdx.x; t < n; t += QMH_WG) m = s[t] > m ? s[t] : m;
         m = qmh_block_max(m, redf);
+        if (s[0] != s[0]) m = s[0];  // the reference's scan starts from x[0]: a NaN there stays
         double sum = 0.0;
         for (int t = threadIdx.x; t < n; t += QMH_WG) sum += (double)qmh_expf(s[t] - m);
         sum = qmh_block_sum_d(sum, red);
