@@ -76,6 +76,35 @@ int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, cons
                            int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
                        int n_kv_heads, int head_dim, int max_seq, void *stream);
+/* ---- batched prefill (qmh_prefill.hip) ---- */
+enum { QMH_PF_STORE = 0, QMH_PF_ADD = 1, QMH_PF_QKV = 2, QMH_PF_SWIGLU = 3 };
+typedef struct {
+    /* weight: tiled codes/scales as for the matvec; il: interleaved W1 | W3 tiles */
+    int dtype;
+    const uint8_t *codes;
+    const uint16_t *scales;
+    int nb, tile_r, il, rows, rows_alloc; /* rows: output rows; rows_alloc: rows with slots */
+    /* activations: Q8_0 codes [nb][PP][32] and scales [nb][PP] of P tokens (PP % 128 == 0) */
+    const int8_t *xc;
+    const float *xd;
+    int PP, P;
+    /* epilogue: out0 row-major [P][ld0]; QKV: q -> out0, k -> out1 ([kvd][max_seq]), v -> out2 */
+    int epi;
+    float *out0, *out1, *out2;
+    int ld0, seg1, seg2;
+    const float *rope;
+    int pos0, head_dim, max_seq, kvd;
+} qmh_pf_args;
+int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tokens, int P, float *X,
+                        void *stream);
+/* rows p < P of x (stride ldx, n values; RMSNorm'd with gain w when w != NULL) -> image codes/scales */
+int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc, float *xd,
+                        int PP, int perm8, void *stream);
+int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream);
+/* causal attention of P tokens at positions pos0.. over the caches; att: scratch [n_heads][P][max_seq] */
+int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P, int pos0,
+                            int n_heads, int n_kv, int hd, int max_seq, float scale, void *stream);
+
 /* argmax over x[n] -> *out_idx; if tokpos != NULL also tokpos[0] = idx, tokpos[1] += 1 and
  * record[step] = idx (when step < record_cap) where step = tokpos[2]++ (device greedy loop state) */
 int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record, int record_cap,

@@ -1,0 +1,395 @@
+// gfx950 batched prefill: P prompt tokens through the model at once, bitwise equal to P
+// sequential forwards (the reference's prompt loop, src/main.c:127-130, calling
+// qm_model_forward, src/model.c:158-191).
+//
+// Exactness, layer by layer:
+//   * activations are quantized per token row exactly as qm_quantize_row_q8 does (src/quant.c);
+//   * a matmul row (r, token p) is the reference's serial chain s = +0; s = s + (float)acc_b *
+//     (dw_b * dx_b) over blocks b in order (src/kernels_scalar.c:12-34). acc_b, the exact int32
+//     dot of one 32-element block, comes from one v_mfma_i32_16x16x32_i8 with a zero
+//     accumulator (16 rows x 16 tokens x one block per instruction); each lane then extends the
+//     float chains of its 4 (row, token) pairs;
+//   * attention scores, softmax and the weighted V sum keep the decode kernels' per-element
+//     orders (serial over head_dim, the reference softmax, serial over positions).
+//
+// MFMA operand layout (v_mfma_i32_16x16x32_i8, checked on the device): A[i][k] in lane
+// i + 16*(k/8), byte k%8; B[k][j] in lane j + 16*(k/8), byte k%8; D[i][j] in lane j + 16*(i/4),
+// element i%4. Any permutation of k applied to both operands leaves the dot unchanged; for
+// Q4_0 weights each 8-element group is taken as [e0 e2 e4 e6 e1 e3 e5 e7] (the low nibbles of
+// 4 bytes, then the high nibbles), and activations are stored in the same order.
+#include "qmh_device.h"
+#include "qmh_launch.h"
+
+#define QMH_Q8 2
+#define QMH_Q4 3
+
+typedef int pf_v4i __attribute__((ext_vector_type(4)));
+
+// ============================================================================ embedding
+
+__global__ void k_pf_embed(const uint8_t *__restrict__ E, int dtype, int dim, int vocab, const int32_t *tokens,
+                           float *X) {
+    const int p = blockIdx.x;
+    int tok = tokens[p];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);  // the host validated the ids
+    const size_t nbr = (size_t)(dim + 31) / 32;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+        const int b = i >> 5, k = i & 31;
+        float v;
+        if (dtype == QMH_Q8) {
+            const uint8_t *blk = E + ((size_t)tok * nbr + b) * 34;
+            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(int8_t)blk[2 + k];
+        } else if (dtype == QMH_Q4) {
+            const uint8_t *blk = E + ((size_t)tok * nbr + b) * 18;
+            const uint8_t byte = blk[2 + (k >> 1)];
+            const int q = (k & 1) ? (byte >> 4) : (byte & 15);
+            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(q - 8);
+        } else {
+            v = ((const float *)E)[(size_t)tok * dim + i];
+        }
+        X[(size_t)p * dim + i] = v;
+    }
+}
+
+extern "C" int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tokens,
+                                   int P, float *X, void *stream) {
+    hipLaunchKernelGGL(k_pf_embed, dim3(P), dim3(256), 0, (hipStream_t)stream, tok_embd, dtype, dim, vocab, tokens, X);
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ activation quantization
+//
+// Row p of x (n values, optionally RMSNorm'd with gain w: src/ops.c:93-98) -> Q8_0 blocks of the
+// token-major-within-block image: codes xc[(b*PP + p)*32 + k], scales xd[b*PP + p] (fp32 of the
+// fp16 d). perm8: codes of each 8-group in the order e0 e2 e4 e6 e1 e3 e5 e7 (Q4_0 consumers).
+// One workgroup per token; 8 lanes per block, 4 values each, as the decode prologue.
+__global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x, int ldx, const float *w, float eps,
+                                                     int n, int8_t *xc, float *xd, int PP, int perm8) {
+    __shared__ double red[16];
+    const int p = blockIdx.x, tid = threadIdx.x, nb = (n + 31) / 32, sub = tid & 7;
+    const float *row = x + (size_t)p * ldx;
+    float inv = 1.0f;
+    if (w) {
+        double ss = 0.0;
+        for (int i = tid; i < n; i += QMH_WG) ss += (double)row[i] * (double)row[i];
+        ss = qmh_block_sum_d(ss, red);
+        const double d = qmh_sum_slack(ss, n);
+        inv = qmh_rms_inv(ss - d, n, eps);
+        if (inv != qmh_rms_inv(ss + d, n, eps)) {  // uniform; serial sum as the reference
+            if (tid == 0) {
+                double s = 0.0;
+                for (int i = 0; i < n; i++) s += (double)row[i] * (double)row[i];
+                red[8] = s;
+            }
+            __syncthreads();
+            inv = qmh_rms_inv(red[8], n, eps);
+        }
+    }
+    for (int b0 = 0; b0 < nb; b0 += QMH_WG / 8) {  // uniform trip count: DPP needs all 8 lanes
+        const int b = b0 + (tid >> 3), i4 = b * 32 + sub * 4;
+        const bool on = b < nb;
+        float v[4], m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i4 + j;
+            float xv = (on && i < n) ? row[i] : 0.0f;
+            if (w) xv = (on && i < n) ? xv * inv * w[i] : 0.0f;  // (x*inv)*w as the reference
+            v[j] = xv;
+            const float av = fabsf(xv);
+            m = av > m ? av : m;
+        }
+        m = qmh_amax8(m);
+        const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
+        int q[4];
+        qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
+        if (on) {
+            int8_t *c = xc + ((size_t)b * PP + p) * 32;
+            if (perm8) {  // elements 8g+e (e = 0..7) at 8g + {0,4,1,5,2,6,3,7}[e]
+                const int g = sub >> 1, e0 = (sub & 1) * 4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int e = e0 + j;
+                    c[8 * g + ((e & 1) ? 4 + (e >> 1) : (e >> 1))] = (int8_t)q[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) c[sub * 4 + j] = (int8_t)q[j];
+            }
+            if (sub == 0) xd[(size_t)b * PP + p] = dd;
+        }
+    }
+}
+
+extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc,
+                                   float *xd, int PP, int perm8, void *stream) {
+    hipLaunchKernelGGL(k_pf_quant, dim3(P), dim3(QMH_WG), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd, PP, perm8);
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ matmul
+//
+// One wave: 16 rows x 16*TW tokens (TW token tiles), all blocks in order; 4 waves per
+// workgroup take consecutive 16-row groups. Operands come straight from memory (weights once
+// per token group, activations from L2), the next block's in flight while the current one runs.
+
+__device__ __forceinline__ long pf_q4_operand(uint32_t w) {
+    // 8 nibbles -> 8 signed int8 (q - 8): low nibbles (e0 e2 e4 e6), then high (e1 e3 e5 e7)
+    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    lo ^= 0x08080808u;  // q - 8 as a 4-bit two's complement value ...
+    hi ^= 0x08080808u;
+    lo |= (lo & 0x08080808u) * 0x1eu;  // ... sign-extended to the byte (0x08 * 0x1e = 0xf0)
+    hi |= (hi & 0x08080808u) * 0x1eu;
+    return (long)(((uint64_t)hi << 32) | lo);
+}
+
+// slot of block b of a weight row: plain tiles, or interleaved (W1 | W3) tiles with tile_r/2
+// rows of each matrix (half 0: W1, 1: W3)
+__device__ __forceinline__ size_t pf_slot(const qmh_pf_args &a, int row, int half, int b) {
+    if (a.il) {
+        const int h = a.tile_r / 2;
+        return ((size_t)(row / h) * a.nb + b) * a.tile_r + row % h + half * h;
+    }
+    return ((size_t)(row / a.tile_r) * a.nb + b) * a.tile_r + row % a.tile_r;
+}
+
+template <int WT, int TW, int NM>  // NM: matrices per wave (2 for the W1 | W3 SwiGLU pair)
+struct PfBlock {
+    long A[NM];
+    float dw[NM][4];
+    long B[TW];
+    float dx[TW];
+};
+
+template <int WT, int TW, int NM>
+__device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, int r0, int t0, PfBlock<WT, TW, NM> &o) {
+    const int l = threadIdx.x & 63, kq = l >> 4;
+    const int row = r0 + (l & 15), grp = r0 + 4 * kq;  // A row; first of the lane's 4 D rows
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        if (row < a.rows_alloc) {
+            const size_t s = pf_slot(a, row, m, b);
+            if (WT == QMH_Q8) o.A[m] = *(const long *)(a.codes + s * 32 + 8 * kq);
+            else o.A[m] = pf_q4_operand(*(const uint32_t *)(a.codes + s * 16 + 4 * kq));
+        } else {
+            o.A[m] = 0;
+        }
+        if (grp < a.rows_alloc) {
+            const uint2 sc = *(const uint2 *)(a.scales + pf_slot(a, grp, m, b));
+            o.dw[m][0] = qmh_h2f((uint16_t)(sc.x & 0xffffu));
+            o.dw[m][1] = qmh_h2f((uint16_t)(sc.x >> 16));
+            o.dw[m][2] = qmh_h2f((uint16_t)(sc.y & 0xffffu));
+            o.dw[m][3] = qmh_h2f((uint16_t)(sc.y >> 16));
+        } else {
+            o.dw[m][0] = o.dw[m][1] = o.dw[m][2] = o.dw[m][3] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TW; tt++) {
+        const int p = t0 + 16 * tt + (l & 15);
+        o.B[tt] = *(const long *)(a.xc + ((size_t)b * a.PP + p) * 32 + 8 * kq);
+        o.dx[tt] = a.xd[(size_t)b * a.PP + p];
+    }
+}
+
+template <int WT, int TW, int NM>
+__global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4;
+    const int r0 = (blockIdx.y * (QMH_WG / 64) + wave) * 16;  // the wave's 16 rows
+    const int t0 = blockIdx.x * 16 * TW;                      // the wave's first token
+    if (r0 >= a.rows) return;
+    float s[NM][TW][4];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int tt = 0; tt < TW; tt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) s[m][tt][e] = 0.0f;
+    PfBlock<WT, TW, NM> cur, nxt;
+    pf_load<WT, TW, NM>(a, 0, r0, t0, cur);
+    for (int b = 0; b < a.nb; b++) {
+        pf_load<WT, TW, NM>(a, b + 1 < a.nb ? b + 1 : b, r0, t0, nxt);
+#pragma unroll
+        for (int tt = 0; tt < TW; tt++) {
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const pf_v4i z = {0, 0, 0, 0};
+                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.A[m], cur.B[tt], z, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[m][tt][e] = s[m][tt][e] + (float)acc[e] * (cur.dw[m][e] * cur.dx[tt]);
+            }
+        }
+        cur = nxt;
+    }
+    // epilogues: lane l holds rows r0 + 4*kq + e (e < 4) of tokens t0 + 16*tt + l%16
+#pragma unroll
+    for (int tt = 0; tt < TW; tt++) {
+        const int p = t0 + 16 * tt + (l & 15);
+        if (p >= a.P) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = r0 + 4 * kq + e;
+            if (r >= a.rows) continue;
+            const float y = s[0][tt][e];
+            if (a.epi == QMH_PF_STORE) {
+                a.out0[(size_t)p * a.ld0 + r] = y;
+            } else if (a.epi == QMH_PF_ADD) {  // x += W x' (src/model.c:179,186)
+                a.out0[(size_t)p * a.ld0 + r] = a.out0[(size_t)p * a.ld0 + r] + y;
+            } else if (a.epi == QMH_PF_SWIGLU) {  // silu(g)*u (src/ops.c:128-133)
+                const float up = s[NM - 1][tt][e];
+                a.out0[(size_t)p * a.ld0 + r] = y / (1.0f + qmh_expf(-y)) * up;
+            } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
+                const int pos = a.pos0 + p;
+                if (r < a.seg2) {
+                    const int local = r < a.seg1 ? r : r - a.seg1;
+                    const float *cs = a.rope + ((size_t)pos * (a.head_dim >> 1) + ((local % a.head_dim) >> 1)) * 2;
+                    const float c = cs[0], sn = cs[1];
+                    const float partner = s[0][tt][e ^ 1];  // rows 2i, 2i+1 share the lane
+                    const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
+                    if (r < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
+                    else a.out1[(size_t)local * a.max_seq + pos] = v;
+                } else {
+                    a.out2[(size_t)pos * a.kvd + (r - a.seg2)] = y;
+                }
+            }
+        }
+    }
+}
+
+extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
+    if (a->PP % 128 || a->P > a->PP || a->nb < 1) return (int)hipErrorInvalidValue;
+    const dim3 grid(a->PP / 128, (a->rows + 63) / 64);
+    hipStream_t s = (hipStream_t)stream;
+    if (a->epi == QMH_PF_SWIGLU) {
+        if (!a->il) return (int)hipErrorInvalidValue;
+        const dim3 g2(a->PP / 64, (a->rows + 63) / 64);
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
+        else if (a->dtype == QMH_Q8) hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
+        else return (int)hipErrorInvalidValue;
+    } else {
+        if (a->il) return (int)hipErrorInvalidValue;
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 8, 1>), grid, dim3(QMH_WG), 0, s, *a);
+        else if (a->dtype == QMH_Q8) hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 8, 1>), grid, dim3(QMH_WG), 0, s, *a);
+        else return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+// ============================================================================ attention
+//
+// Scores of 16 tokens against 256 positions per workgroup (lane = position; 16 serial dot
+// chains over head_dim per lane, K^T read once for the 16 tokens), each times the scale as
+// src/model.c:146. Rows of att: (head, token) with max_seq entries; entries past the token's
+// position are not written.
+#define QMH_PF_TOK 16
+__global__ __launch_bounds__(QMH_WG) void k_pf_scores(const float *__restrict__ Q, const float *__restrict__ Kt,
+                                                      float *att, int P, int pos0, int n_heads, int n_kv, int hd,
+                                                      int max_seq, float scale) {
+    __shared__ float qs[QMH_PF_TOK * 256];  // [token][d], hd <= 256
+    const int h = blockIdx.x, g = blockIdx.y, t = blockIdx.z * QMH_WG + threadIdx.x;
+    const int p0 = g * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
+    if (blockIdx.z * QMH_WG > pos0 + p0 + np - 1) return;  // past every token of the group
+    const int kvh = h / (n_heads / n_kv), D = n_heads * hd;
+    for (int i = threadIdx.x; i < QMH_PF_TOK * hd; i += QMH_WG) {
+        const int k = i / hd, d = i - k * hd;
+        qs[i] = k < np ? Q[(size_t)(p0 + k) * D + h * hd + d] : 0.0f;
+    }
+    __syncthreads();
+    const int tc = t < max_seq ? t : max_seq - 1;
+    const float *kc = Kt + (size_t)kvh * hd * max_seq + tc;
+    float s[QMH_PF_TOK];
+#pragma unroll
+    for (int k = 0; k < QMH_PF_TOK; k++) s[k] = 0.0f;
+    for (int d0 = 0; d0 < hd; d0 += 8) {
+        float kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (d0 + j < hd) {
+#pragma unroll
+                for (int k = 0; k < QMH_PF_TOK; k++) s[k] = s[k] + qs[k * hd + d0 + j] * kv[j];
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < QMH_PF_TOK; k++)
+        if (k < np && t <= pos0 + p0 + k) att[((size_t)h * P + p0 + k) * max_seq + t] = s[k] * scale;
+}
+
+// softmax of one (head, token) row in place (src/ops.c:100-112), as the decode kernels
+__global__ __launch_bounds__(QMH_WG) void k_pf_softmax(float *att, int P, int pos0, int max_seq) {
+    __shared__ double red[16];
+    __shared__ float redf[16];
+    const int h = blockIdx.x, p = blockIdx.y, n = pos0 + p + 1;
+    float *x = att + ((size_t)h * P + p) * max_seq;
+    float m = -__builtin_inff();
+    for (int t = threadIdx.x; t < n; t += QMH_WG) m = x[t] > m ? x[t] : m;
+    m = qmh_block_max(m, redf);
+    if (x[0] != x[0]) m = x[0];  // the reference's scan starts from x[0]: a NaN there stays
+    double sum = 0.0;
+    for (int t = threadIdx.x; t < n; t += QMH_WG) {
+        const float e = qmh_expf(x[t] - m);
+        x[t] = e;
+        sum += (double)e;
+    }
+    sum = qmh_block_sum_d(sum, red);
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
+        if (threadIdx.x == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)x[t];
+            red[8] = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(red[8]);
+    }
+    for (int t = threadIdx.x; t < n; t += QMH_WG) x[t] = x[t] * inv;
+}
+
+// out[token][h*hd + i] = +0 + p_0 v_0[i] + p_1 v_1[i] + ... in position order (src/model.c:147-154);
+// one workgroup per (head, 16 tokens): thread i < hd runs the 16 tokens' chains of column i,
+// probabilities staged through LDS in chunks of 256 positions
+__global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att, const float *__restrict__ V,
+                                                  float *out, int P, int pos0, int n_heads, int n_kv, int hd,
+                                                  int max_seq) {
+    __shared__ float ps[QMH_PF_TOK * QMH_WG];  // [token][t]
+    const int h = blockIdx.x, p0 = blockIdx.y * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
+    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, i = threadIdx.x;
+    const int tmax = pos0 + p0 + np;  // positions 0 .. tmax-1 are used by some token
+    const float *vc = V + (size_t)kvh * hd + (i < hd ? i : 0);
+    float acc[QMH_PF_TOK];
+#pragma unroll
+    for (int k = 0; k < QMH_PF_TOK; k++) acc[k] = 0.0f;
+    for (int c0 = 0; c0 < tmax; c0 += QMH_WG) {
+        __syncthreads();
+        for (int j = threadIdx.x; j < QMH_PF_TOK * QMH_WG; j += QMH_WG) {
+            const int k = j / QMH_WG, t = c0 + (j - k * QMH_WG);
+            ps[j] = (k < np && t <= pos0 + p0 + k) ? att[((size_t)h * P + p0 + k) * max_seq + t] : 0.0f;
+        }
+        __syncthreads();
+        if (i < hd) {
+            const int nt = min(QMH_WG, tmax - c0);
+            for (int t = 0; t < nt; t++) {
+                const float v = vc[(size_t)(c0 + t) * kvd];
+#pragma unroll
+                for (int k = 0; k < QMH_PF_TOK; k++)
+                    if (c0 + t <= pos0 + p0 + k) acc[k] = acc[k] + ps[k * QMH_WG + t] * v;
+            }
+        }
+    }
+    if (i < hd)
+        for (int k = 0; k < np; k++) out[(size_t)(p0 + k) * n_heads * hd + h * hd + i] = acc[k];
+}
+
+extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P,
+                                       int pos0, int n_heads, int n_kv, int hd, int max_seq, float scale,
+                                       void *stream) {
+    if (hd > 256 || hd > QMH_WG || pos0 + P > max_seq || P < 1) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const int ng = (P + QMH_PF_TOK - 1) / QMH_PF_TOK, nz = (pos0 + P + QMH_WG - 1) / QMH_WG;
+    hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
+                       hd, max_seq, scale);
+    hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, P), dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
+    hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd, max_seq);
+    return (int)hipGetLastError();
+}

@@ -383,6 +383,11 @@ struct qmh_model {
     hipGraph_t graph_fwd, graph_greedy;
     hipGraphExec_t exec_fwd, exec_greedy;
     int use_graph; /* 0 when QMH_NO_GRAPH is set: the same kernels, enqueued one by one (profiling) */
+    /* batched prefill (every matrix quantized): up to pf_cap tokens per pass, padded to pf_pp */
+    int pf_ok, pf_cap, pf_pp;
+    int32_t *d_pf_tok, *h_pf_tok;
+    float *d_pf_x, *d_pf_xb, *d_pf_q, *d_pf_hb, *d_pf_att, *d_pf_logits, *d_pf_xd;
+    int8_t *d_pf_xc;
 };
 
 /* the kernels of one decode step, by stage (which) and layer */
@@ -587,12 +592,15 @@ void qmh_model_free(qmh_model *m) {
         free(m->layers);
     }
     weight_release(&m->output);
-    void *dev[] = {m->d_embd, m->d_norms, m->d_rope, m->d_x,      m->d_xb,     m->d_q,      m->d_hb,
-                   m->d_hq,   m->d_att,   m->d_logits, m->d_kt,  m->d_v, m->d_tokpos, m->d_record};
+    void *dev[] = {m->d_embd,   m->d_norms,  m->d_rope,     m->d_x,    m->d_xb,   m->d_q,     m->d_hb,
+                   m->d_hq,     m->d_att,    m->d_logits,   m->d_kt,   m->d_v,    m->d_tokpos, m->d_record,
+                   m->d_pf_tok, m->d_pf_x,   m->d_pf_xb,    m->d_pf_q, m->d_pf_hb, m->d_pf_att, m->d_pf_logits,
+                   m->d_pf_xd,  m->d_pf_xc};
     for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_tokpos) hipHostFree(m->h_tokpos);
     if (m->h_logits) hipHostFree(m->h_logits);
+    if (m->h_pf_tok) hipHostFree(m->h_pf_tok);
     free(m);
 }
 
@@ -703,6 +711,30 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
     HIPCHK(hipHostMalloc((void **)&m->h_tokpos, sizeof(int32_t) * 4 * (size_t)S_, hipHostMallocDefault));
     HIPCHK(hipHostMalloc((void **)&m->h_logits, sizeof(float) * V, hipHostMallocDefault));
+    /* batched prefill buffers (models whose matrices are all quantized) */
+    m->pf_ok = m->output.dtype != QMH_F32 && m->hd <= 256;
+    for (int l = 0; l < c->n_layers && m->pf_ok; l++) {
+        const dev_layer *L = &m->layers[l];
+        m->pf_ok = L->qkv.dtype != QMH_F32 && L->wo.dtype != QMH_F32 && L->w13.dtype != QMH_F32 &&
+                   L->w2.dtype != QMH_F32;
+    }
+    if (m->pf_ok) {
+        m->pf_cap = S_ < 512 ? (int)S_ : 512;
+        m->pf_pp = (m->pf_cap + 127) / 128 * 128;
+        const size_t PP = (size_t)m->pf_pp, nbmax = (size_t)((D > H ? D : H) + 31) / 32;
+        HIPCHK(hipMalloc((void **)&m->d_pf_tok, sizeof(int32_t) * PP));
+        HIPCHK(hipHostMalloc((void **)&m->h_pf_tok, sizeof(int32_t) * PP, hipHostMallocDefault));
+        HIPCHK(hipMalloc((void **)&m->d_pf_x, sizeof(float) * PP * D));
+        HIPCHK(hipMalloc((void **)&m->d_pf_xb, sizeof(float) * PP * D));
+        HIPCHK(hipMalloc((void **)&m->d_pf_q, sizeof(float) * PP * D));
+        HIPCHK(hipMalloc((void **)&m->d_pf_hb, sizeof(float) * PP * H));
+        HIPCHK(hipMalloc((void **)&m->d_pf_att, sizeof(float) * (size_t)c->n_heads * PP * S_));
+        HIPCHK(hipMalloc((void **)&m->d_pf_logits, sizeof(float) * PP * V));
+        HIPCHK(hipMalloc((void **)&m->d_pf_xc, 32 * nbmax * PP));
+        HIPCHK(hipMalloc((void **)&m->d_pf_xd, sizeof(float) * nbmax * PP));
+        HIPCHK(hipMemsetAsync(m->d_pf_xc, 0, 32 * nbmax * PP, g_stream));
+        HIPCHK(hipMemsetAsync(m->d_pf_xd, 0, sizeof(float) * nbmax * PP, g_stream));
+    }
     HIPCHK(hipStreamSynchronize(g_stream));
     m->use_graph = getenv("QMH_NO_GRAPH") == NULL;
     if (m->use_graph && capture(m, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
@@ -799,10 +831,111 @@ float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
     return m->h_logits;
 }
 
+/* the batched matmul over the prefill activation image (d_pf_xc/xd) with weight w */
+static void pf_args_for(const qmh_model *m, const struct qmh_weight *w, int P, qmh_pf_args *a) {
+    memset(a, 0, sizeof *a);
+    a->dtype = w->dtype;
+    a->codes = w->codes;
+    a->scales = w->scales;
+    a->nb = w->nb;
+    a->tile_r = w->tile_r;
+    a->rows = (int)w->rows;
+    a->xc = m->d_pf_xc;
+    a->xd = m->d_pf_xd;
+    a->PP = m->pf_pp;
+    a->P = P;
+}
+
+/* one layer for P tokens at positions pos.. (src/model.c:164-187, token by token in the reference) */
+static int pf_layer(qmh_model *m, int l, int P, int pos, hipStream_t s) {
+    const qmh_config *c = &m->cfg;
+    const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq, PP = m->pf_pp;
+    dev_layer *L = &m->layers[l];
+    float *kl = m->d_kt + (size_t)l * S_ * m->kvd, *vl = m->d_v + (size_t)l * S_ * m->kvd;
+    qmh_pf_args a;
+    /* q, k, v = W rmsnorm(x); rope; k, v -> caches */
+    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * l) * D, c->norm_eps, D, P, m->d_pf_xc, m->d_pf_xd,
+                             PP, L->qkv.dtype == QMH_Q4_0, s));
+    pf_args_for(m, &L->qkv, P, &a);
+    a.rows_alloc = L->qkv.ntiles * L->qkv.tile_r;
+    a.epi = QMH_PF_QKV;
+    a.out0 = m->d_pf_q;
+    a.ld0 = D;
+    a.out1 = kl;
+    a.out2 = vl;
+    a.seg1 = D;
+    a.seg2 = D + m->kvd;
+    a.rope = m->d_rope;
+    a.pos0 = pos;
+    a.head_dim = m->hd;
+    a.max_seq = S_;
+    a.kvd = m->kvd;
+    LCHK(qmh_launch_pf_gemm(&a, s));
+    LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads, m->hd,
+                                 S_, 1.0f / sqrtf((float)m->hd), s));
+    /* x += Wo xb */
+    LCHK(qmh_launch_pf_quant(m->d_pf_xb, D, NULL, 0.0f, D, P, m->d_pf_xc, m->d_pf_xd, PP, L->wo.dtype == QMH_Q4_0, s));
+    pf_args_for(m, &L->wo, P, &a);
+    a.rows_alloc = L->wo.ntiles * L->wo.tile_r;
+    a.epi = QMH_PF_ADD;
+    a.out0 = m->d_pf_x;
+    a.ld0 = D;
+    LCHK(qmh_launch_pf_gemm(&a, s));
+    /* hb = silu(W1 rmsnorm(x)) * (W3 rmsnorm(x)) */
+    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * l + 1) * D, c->norm_eps, D, P, m->d_pf_xc,
+                             m->d_pf_xd, PP, L->w13.dtype == QMH_Q4_0, s));
+    pf_args_for(m, &L->w13, P, &a);
+    a.il = 1;
+    a.rows_alloc = L->w13.ntiles * (L->w13.tile_r / 2);
+    a.epi = QMH_PF_SWIGLU;
+    a.out0 = m->d_pf_hb;
+    a.ld0 = H;
+    LCHK(qmh_launch_pf_gemm(&a, s));
+    /* x += W2 hb */
+    LCHK(qmh_launch_pf_quant(m->d_pf_hb, H, NULL, 0.0f, H, P, m->d_pf_xc, m->d_pf_xd, PP, L->w2.dtype == QMH_Q4_0, s));
+    pf_args_for(m, &L->w2, P, &a);
+    a.rows_alloc = L->w2.ntiles * L->w2.tile_r;
+    a.epi = QMH_PF_ADD;
+    a.out0 = m->d_pf_x;
+    a.ld0 = D;
+    LCHK(qmh_launch_pf_gemm(&a, s));
+    return 0;
+}
+
+/* the prompt in passes of up to pf_cap tokens; logits (P x vocab) only when asked for */
+static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits) {
+    const qmh_config *c = &m->cfg;
+    const int D = c->dim, V = c->vocab_size;
+    for (int32_t c0 = 0; c0 < n; c0 += m->pf_cap) {
+        const int P = n - c0 < m->pf_cap ? n - c0 : m->pf_cap, pos = pos0 + c0;
+        memcpy(m->h_pf_tok, tokens + c0, sizeof(int32_t) * (size_t)P);
+        HIPCHK(hipMemcpyAsync(m->d_pf_tok, m->h_pf_tok, sizeof(int32_t) * (size_t)P, hipMemcpyHostToDevice, g_stream));
+        LCHK(qmh_launch_pf_embed(m->d_embd, m->emb_dtype, D, V, m->d_pf_tok, P, m->d_pf_x, g_stream));
+        for (int l = 0; l < c->n_layers; l++)
+            if (pf_layer(m, l, P, pos, g_stream)) return -1;
+        if (logits) { /* logits = Woutput rmsnorm(x) for every position (src/model.c:188-189) */
+            qmh_pf_args a;
+            LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * c->n_layers) * D, c->norm_eps, D, P,
+                                     m->d_pf_xc, m->d_pf_xd, m->pf_pp, m->output.dtype == QMH_Q4_0, g_stream));
+            pf_args_for(m, &m->output, P, &a);
+            a.rows_alloc = m->output.ntiles * m->output.tile_r;
+            a.epi = QMH_PF_STORE;
+            a.out0 = m->d_pf_logits;
+            a.ld0 = V;
+            LCHK(qmh_launch_pf_gemm(&a, g_stream));
+            HIPCHK(hipMemcpyAsync(logits + (size_t)c0 * V, m->d_pf_logits, sizeof(float) * (size_t)P * V,
+                                  hipMemcpyDeviceToHost, g_stream));
+        }
+        HIPCHK(hipStreamSynchronize(g_stream)); /* h_pf_tok is reused by the next pass */
+    }
+    return 0;
+}
+
 int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits) {
     if (!m || !tokens || n < 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.max_seq) return fail("prefill: bad range");
     for (int32_t i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) return fail("prefill: token %d out of range", tokens[i]);
+    if (m->pf_ok && getenv("QMH_PREFILL_SEQ") == NULL) return pf_batched(m, tokens, n, pos0, logits);
     const size_t V = (size_t)m->cfg.vocab_size;
     for (int32_t i = 0; i < n; i++) {
         int32_t *slot = m->h_tokpos + 4 * (size_t)i;
