@@ -120,3 +120,33 @@ def test_baseline_config_vs_reference(gpu, tmp_path, name):
         for g in range(w.n_gen):
             got.append(m.forward(toks[g], w.n_prompt + g).copy())
         assert np.array_equal(bits(np.stack(got)), bits(rl[w.n_prompt:]))
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
+    """The batched prefill (int8 MFMA matmuls, batched attention) against the one-token-at-a-time
+    path on the same model: every position's logits, the KV cache (through the decode step that
+    follows), across a second pass (600 tokens > 512 per pass), an odd-sized continuation at
+    pos0 > 0, and GQA with head_dim 32."""
+    import os
+
+    path = str(tmp_path / f"pf_{wt}.qlm")
+    cfg = gpu.QmhConfig(dim=128, hidden_dim=344, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=700,
+                        rope_theta=10000.0, norm_eps=1e-5)
+    gpu.gen_model(path, cfg, wt, seed=31, threads=4)
+    prompt, more = gpu.prompt_ids(600, 300, seed=8), gpu.prompt_ids(30, 300, seed=12)
+    runs = []
+    for seq in (False, True):
+        if seq:
+            os.environ["QMH_PREFILL_SEQ"] = "1"
+        try:
+            with gpu.Model.load(path) as m:
+                say(f"case {wt}: prefill {'sequential' if seq else 'batched'}")
+                a = m.prefill(prompt, 0, want_logits=True)
+                b = m.prefill(more, 600, want_logits=True)
+                c = m.forward(7, 630).copy()
+                runs.append((a, b, c))
+        finally:
+            os.environ.pop("QMH_PREFILL_SEQ", None)
+    for got, want in zip(runs[0], runs[1]):
+        assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
