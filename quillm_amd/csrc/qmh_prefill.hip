@@ -142,52 +142,50 @@ __device__ __forceinline__ long pf_q4_operand(uint32_t w) {
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
-// slot of block b of a weight row: plain tiles, or interleaved (W1 | W3) tiles with tile_r/2
-// rows of each matrix (half 0: W1, 1: W3)
-__device__ __forceinline__ size_t pf_slot(const qmh_pf_args &a, int row, int half, int b) {
+// slot of block 0 of a weight row: plain tiles, or interleaved (W1 | W3) tiles with tile_r/2
+// rows of each matrix (half 0: W1, 1: W3); block b adds b*tile_r
+__device__ __forceinline__ uint32_t pf_slot0(const qmh_pf_args &a, int row, int half) {
     if (a.il) {
         const int h = a.tile_r / 2;
-        return ((size_t)(row / h) * a.nb + b) * a.tile_r + row % h + half * h;
+        return (uint32_t)(row / h) * a.nb * a.tile_r + row % h + half * h;
     }
-    return ((size_t)(row / a.tile_r) * a.nb + b) * a.tile_r + row % a.tile_r;
+    return (uint32_t)(row / a.tile_r) * a.nb * a.tile_r + row % a.tile_r;
 }
 
 template <int WT, int TW, int NM>  // NM: matrices per wave (2 for the W1 | W3 SwiGLU pair)
 struct PfBlock {
     long A[NM];
-    float dw[NM][4];
+    uint2 sc[NM];
     long B[TW];
     float dx[TW];
 };
 
+// Per-lane byte/element offsets of the operands, fixed over the blocks: the loop adds only the
+// block's uniform base, so the loads take a scalar base and these offsets.
+template <int NM>
+struct PfLane {
+    uint32_t a[NM], s[NM];  // weight codes (bytes), scales (elements) at block 0
+    bool ain[NM], sin[NM];  // the row (group) has slots
+    uint32_t x, d;          // activation codes (bytes), scales (elements) of token tile 0
+};
+
 template <int WT, int TW, int NM>
-__device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, int r0, int t0, PfBlock<WT, TW, NM> &o) {
-    const int l = threadIdx.x & 63, kq = l >> 4;
-    const int row = r0 + (l & 15), grp = r0 + 4 * kq;  // A row; first of the lane's 4 D rows
+__device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLane<NM> &ln, PfBlock<WT, TW, NM> &o) {
+    constexpr int CB = WT == QMH_Q8 ? 32 : 16;
+    const uint8_t *cb = a.codes + (size_t)b * a.tile_r * CB;
+    const uint16_t *sb = a.scales + (size_t)b * a.tile_r;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-        if (row < a.rows_alloc) {
-            const size_t s = pf_slot(a, row, m, b);
-            if (WT == QMH_Q8) o.A[m] = *(const long *)(a.codes + s * 32 + 8 * kq);
-            else o.A[m] = pf_q4_operand(*(const uint32_t *)(a.codes + s * 16 + 4 * kq));
-        } else {
-            o.A[m] = 0;
-        }
-        if (grp < a.rows_alloc) {
-            const uint2 sc = *(const uint2 *)(a.scales + pf_slot(a, grp, m, b));
-            o.dw[m][0] = qmh_h2f((uint16_t)(sc.x & 0xffffu));
-            o.dw[m][1] = qmh_h2f((uint16_t)(sc.x >> 16));
-            o.dw[m][2] = qmh_h2f((uint16_t)(sc.y & 0xffffu));
-            o.dw[m][3] = qmh_h2f((uint16_t)(sc.y >> 16));
-        } else {
-            o.dw[m][0] = o.dw[m][1] = o.dw[m][2] = o.dw[m][3] = 0.0f;
-        }
+        if (WT == QMH_Q8) o.A[m] = ln.ain[m] ? *(const long *)(cb + ln.a[m]) : 0;
+        else o.A[m] = ln.ain[m] ? pf_q4_operand(*(const uint32_t *)(cb + ln.a[m])) : 0;
+        o.sc[m] = ln.sin[m] ? *(const uint2 *)(sb + ln.s[m]) : make_uint2(0u, 0u);
     }
+    const int8_t *xb = a.xc + (size_t)b * a.PP * 32;
+    const float *db = a.xd + (size_t)b * a.PP;
 #pragma unroll
     for (int tt = 0; tt < TW; tt++) {
-        const int p = t0 + 16 * tt + (l & 15);
-        o.B[tt] = *(const long *)(a.xc + ((size_t)b * a.PP + p) * 32 + 8 * kq);
-        o.dx[tt] = a.xd[(size_t)b * a.PP + p];
+        o.B[tt] = *(const long *)(xb + ln.x + tt * 512);
+        o.dx[tt] = db[ln.d + tt * 16];
     }
 }
 
@@ -197,6 +195,18 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
     const int r0 = (blockIdx.y * (QMH_WG / 64) + wave) * 16;  // the wave's 16 rows
     const int t0 = blockIdx.x * 16 * TW;                      // the wave's first token
     if (r0 >= a.rows) return;
+    constexpr int CB = WT == QMH_Q8 ? 32 : 16;
+    PfLane<NM> ln;
+    const int row = r0 + (l & 15), grp = r0 + 4 * kq;  // A row; first of the lane's 4 D rows
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        ln.ain[m] = row < a.rows_alloc;
+        ln.sin[m] = grp < a.rows_alloc;
+        ln.a[m] = pf_slot0(a, ln.ain[m] ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
+        ln.s[m] = pf_slot0(a, ln.sin[m] ? grp : 0, m);
+    }
+    ln.x = (uint32_t)(t0 + (l & 15)) * 32 + 8 * kq;
+    ln.d = (uint32_t)(t0 + (l & 15));
     float s[NM][TW][4];
 #pragma unroll
     for (int m = 0; m < NM; m++)
@@ -205,18 +215,26 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
 #pragma unroll
             for (int e = 0; e < 4; e++) s[m][tt][e] = 0.0f;
     PfBlock<WT, TW, NM> cur, nxt;
-    pf_load<WT, TW, NM>(a, 0, r0, t0, cur);
+    pf_load<WT, TW, NM>(a, 0, ln, cur);
     for (int b = 0; b < a.nb; b++) {
-        pf_load<WT, TW, NM>(a, b + 1 < a.nb ? b + 1 : b, r0, t0, nxt);
+        pf_load<WT, TW, NM>(a, b + 1 < a.nb ? b + 1 : b, ln, nxt);
+        pf_v4i acc[NM][TW];
 #pragma unroll
-        for (int tt = 0; tt < TW; tt++) {
+        for (int tt = 0; tt < TW; tt++)
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const pf_v4i z = {0, 0, 0, 0};
-                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.A[m], cur.B[tt], z, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; e++) s[m][tt][e] = s[m][tt][e] + (float)acc[e] * (cur.dw[m][e] * cur.dx[tt]);
+                acc[m][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.A[m], cur.B[tt], z, 0, 0, 0);
             }
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m].x >> 16)),
+                                 qmh_h2f((uint16_t)(cur.sc[m].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m].y >> 16))};
+#pragma unroll
+            for (int tt = 0; tt < TW; tt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    s[m][tt][e] = s[m][tt][e] + (float)acc[m][tt][e] * (dw[e] * cur.dx[tt]);
         }
         cur = nxt;
     }
@@ -256,12 +274,12 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
 }
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
-    if (a->PP % 128 || a->P > a->PP || a->nb < 1) return (int)hipErrorInvalidValue;
-    const dim3 grid(a->PP / 128, (a->rows + 63) / 64);
+    if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
+    const dim3 grid((a->P + 127) / 128, (a->rows + 63) / 64);  // token groups past P are not launched
     hipStream_t s = (hipStream_t)stream;
     if (a->epi == QMH_PF_SWIGLU) {
         if (!a->il) return (int)hipErrorInvalidValue;
-        const dim3 g2(a->PP / 64, (a->rows + 63) / 64);
+        const dim3 g2((a->P + 63) / 64, (a->rows + 63) / 64);
         if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
         else if (a->dtype == QMH_Q8) hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
         else return (int)hipErrorInvalidValue;
