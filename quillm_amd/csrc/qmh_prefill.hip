@@ -365,44 +365,78 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_softmax(float *att, int P, int po
 }
 
 // out[token][h*hd + i] = +0 + p_0 v_0[i] + p_1 v_1[i] + ... in position order (src/model.c:147-154);
-// one workgroup per (head, 16 tokens): thread i < hd runs the 16 tokens' chains of column i,
-// probabilities staged through LDS in chunks of 256 positions
+// one workgroup per (head, 16 tokens), head_dim <= 128. V and the probabilities pass through LDS
+// in chunks of 64 positions (cooperative float4 loads, the next chunk's held in registers while
+// the current one is used); thread (i, half) runs column i's chains of tokens 8*half .. +7.
+#define QMH_PF_VC 64
 __global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att, const float *__restrict__ V,
                                                   float *out, int P, int pos0, int n_heads, int n_kv, int hd,
                                                   int max_seq) {
-    __shared__ float ps[QMH_PF_TOK * QMH_WG];  // [token][t]
+    __shared__ __align__(16) float ps[QMH_PF_TOK * QMH_PF_VC];  // [token][t]
+    __shared__ __align__(16) float vs[QMH_PF_VC * 128];         // [t][column]
     const int h = blockIdx.x, p0 = blockIdx.y * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
-    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, i = threadIdx.x;
+    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, tid = threadIdx.x;
     const int tmax = pos0 + p0 + np;  // positions 0 .. tmax-1 are used by some token
-    const float *vc = V + (size_t)kvh * hd + (i < hd ? i : 0);
-    float acc[QMH_PF_TOK];
+    const float *vbase = V + (size_t)kvh * hd;
+    const int hd4 = hd >> 2;
+    constexpr int VR = QMH_PF_VC * 128 / 4 / QMH_WG;     // float4 of V per thread per chunk
+    constexpr int PR = QMH_PF_TOK * QMH_PF_VC / QMH_WG;  // probabilities per thread per chunk
+    float4 vr[VR];
+    float pr[PR];
+    auto load = [&](int c0) {
 #pragma unroll
-    for (int k = 0; k < QMH_PF_TOK; k++) acc[k] = 0.0f;
-    for (int c0 = 0; c0 < tmax; c0 += QMH_WG) {
-        __syncthreads();
-        for (int j = threadIdx.x; j < QMH_PF_TOK * QMH_WG; j += QMH_WG) {
-            const int k = j / QMH_WG, t = c0 + (j - k * QMH_WG);
-            ps[j] = (k < np && t <= pos0 + p0 + k) ? att[((size_t)h * P + p0 + k) * max_seq + t] : 0.0f;
+        for (int k = 0; k < VR; k++) {
+            const int e = k * QMH_WG + tid, t = e >> 5, c4 = e & 31;  // 32 float4 slots per row
+            const int tc = c0 + t < tmax ? c0 + t : tmax - 1;
+            vr[k] = c4 < hd4 ? *(const float4 *)(vbase + (size_t)tc * kvd + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+#pragma unroll
+        for (int k = 0; k < PR; k++) {
+            const int e = k * QMH_WG + tid, kk = e / QMH_PF_VC, t = c0 + e % QMH_PF_VC;
+            pr[k] = (kk < np && t <= pos0 + p0 + kk) ? att[((size_t)h * P + p0 + kk) * max_seq + t] : 0.0f;
+        }
+    };
+    const int i = tid & 127, half = tid >> 7;
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = 0.0f;
+    load(0);
+    for (int c0 = 0; c0 < tmax; c0 += QMH_PF_VC) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * QMH_WG + tid;
+            *(float4 *)(vs + (e >> 5) * 128 + 4 * (e & 31)) = vr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < PR; k++) ps[k * QMH_WG + tid] = pr[k];
+        if (c0 + QMH_PF_VC < tmax) load(c0 + QMH_PF_VC);
         __syncthreads();
         if (i < hd) {
-            const int nt = min(QMH_WG, tmax - c0);
+            const int nt = min(QMH_PF_VC, tmax - c0);
             for (int t = 0; t < nt; t++) {
-                const float v = vc[(size_t)(c0 + t) * kvd];
+                const float v = vs[t * 128 + i];
+                const int kmin = c0 + t - (pos0 + p0);  // tokens kk >= kmin see position c0 + t
 #pragma unroll
-                for (int k = 0; k < QMH_PF_TOK; k++)
-                    if (c0 + t <= pos0 + p0 + k) acc[k] = acc[k] + ps[k * QMH_WG + t] * v;
+                for (int k = 0; k < 8; k++) {
+                    const int kk = 8 * half + k;
+                    if (kk >= kmin) acc[k] = acc[k] + ps[kk * QMH_PF_VC + t] * v;
+                }
             }
         }
     }
     if (i < hd)
-        for (int k = 0; k < np; k++) out[(size_t)(p0 + k) * n_heads * hd + h * hd + i] = acc[k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int kk = 8 * half + k;
+            if (kk < np) out[(size_t)(p0 + kk) * n_heads * hd + h * hd + i] = acc[k];
+        }
 }
 
 extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P,
                                        int pos0, int n_heads, int n_kv, int hd, int max_seq, float scale,
                                        void *stream) {
-    if (hd > 256 || hd > QMH_WG || pos0 + P > max_seq || P < 1) return (int)hipErrorInvalidValue;
+    if (hd > 128 || hd % 4 || pos0 + P > max_seq || P < 1) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const int ng = (P + QMH_PF_TOK - 1) / QMH_PF_TOK, nz = (pos0 + P + QMH_WG - 1) / QMH_WG;
     hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
