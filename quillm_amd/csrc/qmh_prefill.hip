@@ -128,17 +128,16 @@ extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, floa
 
 // ============================================================================ matmul
 //
-// One wave: 16 rows x 16*TW tokens (TW token tiles), all blocks in order; 4 waves per
-// workgroup take consecutive 16-row groups. Operands come straight from memory (weights once
-// per token group, activations from L2), the next block's in flight while the current one runs.
+// One wave: NR 16-row tiles x TW 16-token tiles, all blocks in order; 4 waves per workgroup
+// take consecutive 16*NR-row groups of one token group. Operands come straight from memory
+// (weights once per token group, activations from L2), PD blocks ahead of the multiplies.
 
 __device__ __forceinline__ long pf_q4_operand(uint32_t w) {
-    // 8 nibbles -> 8 signed int8 (q - 8): low nibbles (e0 e2 e4 e6), then high (e1 e3 e5 e7)
-    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-    lo ^= 0x08080808u;  // q - 8 as a 4-bit two's complement value ...
-    hi ^= 0x08080808u;
-    lo |= (lo & 0x08080808u) * 0x1eu;  // ... sign-extended to the byte (0x08 * 0x1e = 0xf0)
-    hi |= (hi & 0x08080808u) * 0x1eu;
+    // 8 nibbles -> 8 signed int8 (q - 8): low nibbles (e0 e2 e4 e6), then high (e1 e3 e5 e7).
+    // Per byte, q + 0x78 stays below 0x100 (no carry into the next byte), and flipping its top
+    // bit gives q - 8 in two's complement: 0 -> 0xf8, 8 -> 0x00, 15 -> 0x07.
+    const uint32_t lo = ((w & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+    const uint32_t hi = (((w >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
@@ -152,34 +151,42 @@ __device__ __forceinline__ uint32_t pf_slot0(const qmh_pf_args &a, int row, int 
     return (uint32_t)(row / a.tile_r) * a.nb * a.tile_r + row % a.tile_r;
 }
 
-template <int WT, int TW, int NM>  // NM: matrices per wave (2 for the W1 | W3 SwiGLU pair)
+// NM: matrices per wave (2 for the W1 | W3 SwiGLU pair); NR: 16-row tiles per wave (each
+// activation operand feeds NM*NR MFMAs); TW: 16-token tiles per wave
+template <int NM, int NR, int TW>
 struct PfBlock {
-    long A[NM];
-    uint2 sc[NM];
+    long A[NM][NR];   // raw weight codes: 8 int8 (Q8_0) or 4 nibble bytes (Q4_0, low word)
+    uint2 sc[NM][NR];
     long B[TW];
     float dx[TW];
 };
 
 // Per-lane byte/element offsets of the operands, fixed over the blocks: the loop adds only the
-// block's uniform base, so the loads take a scalar base and these offsets.
-template <int NM>
+// block's uniform base, so the loads take a scalar base and these offsets. Rows past the
+// allocated slots read row 0 instead: each D row depends only on its own A row, and those rows
+// are never stored.
+template <int NM, int NR>
 struct PfLane {
-    uint32_t a[NM], s[NM];  // weight codes (bytes), scales (elements) at block 0
-    bool ain[NM], sin[NM];  // the row (group) has slots
-    uint32_t x, d;          // activation codes (bytes), scales (elements) of token tile 0
+    uint32_t a[NM][NR], s[NM][NR];  // weight codes (bytes), scales (elements) at block 0
+    uint32_t x, d;                  // activation codes (bytes), scales (elements) of token tile 0
 };
 
-template <int WT, int TW, int NM>
-__device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLane<NM> &ln, PfBlock<WT, TW, NM> &o) {
+// Loads only: no value is used here, so the wait for these loads falls where the block is
+// multiplied, PD blocks later.
+template <int WT, int NM, int NR, int TW>
+__device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLane<NM, NR> &ln,
+                                        PfBlock<NM, NR, TW> &o) {
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;
     const uint8_t *cb = a.codes + (size_t)b * a.tile_r * CB;
     const uint16_t *sb = a.scales + (size_t)b * a.tile_r;
 #pragma unroll
-    for (int m = 0; m < NM; m++) {
-        if (WT == QMH_Q8) o.A[m] = ln.ain[m] ? *(const long *)(cb + ln.a[m]) : 0;
-        else o.A[m] = ln.ain[m] ? pf_q4_operand(*(const uint32_t *)(cb + ln.a[m])) : 0;
-        o.sc[m] = ln.sin[m] ? *(const uint2 *)(sb + ln.s[m]) : make_uint2(0u, 0u);
-    }
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            if (WT == QMH_Q8) o.A[m][r] = *(const long *)(cb + ln.a[m][r]);
+            else o.A[m][r] = (long)*(const uint32_t *)(cb + ln.a[m][r]);
+            o.sc[m][r] = *(const uint2 *)(sb + ln.s[m][r]);
+        }
     const int8_t *xb = a.xc + (size_t)b * a.PP * 32;
     const float *db = a.xd + (size_t)b * a.PP;
 #pragma unroll
@@ -189,105 +196,130 @@ __device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLan
     }
 }
 
-template <int WT, int TW, int NM>
-__global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4;
-    const int r0 = (blockIdx.y * (QMH_WG / 64) + wave) * 16;  // the wave's 16 rows
-    const int t0 = blockIdx.x * 16 * TW;                      // the wave's first token
-    if (r0 >= a.rows) return;
-    constexpr int CB = WT == QMH_Q8 ? 32 : 16;
-    PfLane<NM> ln;
-    const int row = r0 + (l & 15), grp = r0 + 4 * kq;  // A row; first of the lane's 4 D rows
-#pragma unroll
-    for (int m = 0; m < NM; m++) {
-        ln.ain[m] = row < a.rows_alloc;
-        ln.sin[m] = grp < a.rows_alloc;
-        ln.a[m] = pf_slot0(a, ln.ain[m] ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
-        ln.s[m] = pf_slot0(a, ln.sin[m] ? grp : 0, m);
-    }
-    ln.x = (uint32_t)(t0 + (l & 15)) * 32 + 8 * kq;
-    ln.d = (uint32_t)(t0 + (l & 15));
-    float s[NM][TW][4];
+// one block into the chains: s = s + (float)acc * (dw * dx) per (row, token) pair
+template <int WT, int NM, int NR, int TW>
+__device__ __forceinline__ void pf_mul(const PfBlock<NM, NR, TW> &cur, float (&s)[NM][NR][TW][4]) {
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-        for (int tt = 0; tt < TW; tt++)
+        for (int r = 0; r < NR; r++) {
+            const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m][r].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].x >> 16)),
+                                 qmh_h2f((uint16_t)(cur.sc[m][r].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].y >> 16))};
+            const long Am = WT == QMH_Q8 ? cur.A[m][r] : pf_q4_operand((uint32_t)cur.A[m][r]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) s[m][tt][e] = 0.0f;
-    PfBlock<WT, TW, NM> cur, nxt;
-    pf_load<WT, TW, NM>(a, 0, ln, cur);
-    for (int b = 0; b < a.nb; b++) {
-        pf_load<WT, TW, NM>(a, b + 1 < a.nb ? b + 1 : b, ln, nxt);
-        pf_v4i acc[NM][TW];
-#pragma unroll
-        for (int tt = 0; tt < TW; tt++)
-#pragma unroll
-            for (int m = 0; m < NM; m++) {
+            for (int tt = 0; tt < TW; tt++) {
                 const pf_v4i z = {0, 0, 0, 0};
-                acc[m][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.A[m], cur.B[tt], z, 0, 0, 0);
+                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, cur.B[tt], z, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[m][r][tt][e] = s[m][r][tt][e] + (float)acc[e] * (dw[e] * cur.dx[tt]);
             }
+        }
+}
+
+template <int WT, int NM, int NR, int TW, int PD>
+__global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4;
+    const int r0 = (blockIdx.y * (QMH_WG / 64) + wave) * 16 * NR;  // the wave's 16*NR rows
+    const int t0 = blockIdx.x * 16 * TW;                           // the wave's first token
+    if (r0 >= a.rows) return;
+    constexpr int CB = WT == QMH_Q8 ? 32 : 16;
+    PfLane<NM, NR> ln;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int row = r0 + 16 * r + (l & 15), grp = r0 + 16 * r + 4 * kq;  // A row; first D row
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m].x >> 16)),
-                                 qmh_h2f((uint16_t)(cur.sc[m].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m].y >> 16))};
+            ln.a[m][r] = pf_slot0(a, row < a.rows_alloc ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
+            ln.s[m][r] = pf_slot0(a, grp < a.rows_alloc ? grp : 0, m);
+        }
+    }
+    ln.x = (uint32_t)(t0 + (l & 15)) * 32 + 8 * kq;
+    ln.d = (uint32_t)(t0 + (l & 15));
+    float s[NM][NR][TW][4];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < NR; r++)
 #pragma unroll
             for (int tt = 0; tt < TW; tt++)
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    s[m][tt][e] = s[m][tt][e] + (float)acc[m][tt][e] * (dw[e] * cur.dx[tt]);
+                for (int e = 0; e < 4; e++) s[m][r][tt][e] = 0.0f;
+    // PD blocks in flight ahead of the one multiplied: a ring of PD + 1 operand sets indexed
+    // statically (the group loop is unrolled PD + 1 times), so no operand is copied and each
+    // wait is for loads issued PD blocks earlier. Invariant at the top of a group starting at
+    // block b0: ring[j] holds block b0 + j, j < PD.
+    PfBlock<NM, NR, TW> ring[PD + 1];
+#pragma unroll
+    for (int j = 0; j < PD; j++) pf_load<WT, NM, NR, TW>(a, j < a.nb ? j : a.nb - 1, ln, ring[j]);
+    int b0 = 0;
+    for (; b0 + PD < a.nb; b0 += PD + 1) {
+#pragma unroll
+        for (int j = 0; j <= PD; j++) {
+            const int bn = b0 + j + PD;
+            pf_load<WT, NM, NR, TW>(a, bn < a.nb ? bn : a.nb - 1, ln, ring[(j + PD) % (PD + 1)]);
+            pf_mul<WT, NM, NR, TW>(ring[j], s);
         }
-        cur = nxt;
     }
-    // epilogues: lane l holds rows r0 + 4*kq + e (e < 4) of tokens t0 + 16*tt + l%16
 #pragma unroll
-    for (int tt = 0; tt < TW; tt++) {
-        const int p = t0 + 16 * tt + (l & 15);
-        if (p >= a.P) continue;
+    for (int j = 0; j < PD; j++)
+        if (b0 + j < a.nb) pf_mul<WT, NM, NR, TW>(ring[j], s);
+    // epilogues: lane l holds rows r0 + 16*r + 4*kq + e (e < 4) of tokens t0 + 16*tt + l%16
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int r = r0 + 4 * kq + e;
-            if (r >= a.rows) continue;
-            const float y = s[0][tt][e];
-            if (a.epi == QMH_PF_STORE) {
-                a.out0[(size_t)p * a.ld0 + r] = y;
-            } else if (a.epi == QMH_PF_ADD) {  // x += W x' (src/model.c:179,186)
-                a.out0[(size_t)p * a.ld0 + r] = a.out0[(size_t)p * a.ld0 + r] + y;
-            } else if (a.epi == QMH_PF_SWIGLU) {  // silu(g)*u (src/ops.c:128-133)
-                const float up = s[NM - 1][tt][e];
-                a.out0[(size_t)p * a.ld0 + r] = y / (1.0f + qmh_expf(-y)) * up;
-            } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
-                const int pos = a.pos0 + p;
-                if (r < a.seg2) {
-                    const int local = r < a.seg1 ? r : r - a.seg1;
-                    const float *cs = a.rope + ((size_t)pos * (a.head_dim >> 1) + ((local % a.head_dim) >> 1)) * 2;
-                    const float c = cs[0], sn = cs[1];
-                    const float partner = s[0][tt][e ^ 1];  // rows 2i, 2i+1 share the lane
-                    const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
-                    if (r < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
-                    else a.out1[(size_t)local * a.max_seq + pos] = v;
-                } else {
-                    a.out2[(size_t)pos * a.kvd + (r - a.seg2)] = y;
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int tt = 0; tt < TW; tt++) {
+            const int p = t0 + 16 * tt + (l & 15);
+            if (p >= a.P) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int row = r0 + 16 * r + 4 * kq + e;
+                if (row >= a.rows) continue;
+                const float y = s[0][r][tt][e];
+                if (a.epi == QMH_PF_STORE) {
+                    a.out0[(size_t)p * a.ld0 + row] = y;
+                } else if (a.epi == QMH_PF_ADD) {  // x += W x' (src/model.c:179,186)
+                    a.out0[(size_t)p * a.ld0 + row] = a.out0[(size_t)p * a.ld0 + row] + y;
+                } else if (a.epi == QMH_PF_SWIGLU) {  // silu(g)*u (src/ops.c:128-133)
+                    const float up = s[NM - 1][r][tt][e];
+                    a.out0[(size_t)p * a.ld0 + row] = y / (1.0f + qmh_expf(-y)) * up;
+                } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
+                    const int pos = a.pos0 + p;
+                    if (row < a.seg2) {
+                        const int local = row < a.seg1 ? row : row - a.seg1;
+                        const float *cs =
+                            a.rope + ((size_t)pos * (a.head_dim >> 1) + ((local % a.head_dim) >> 1)) * 2;
+                        const float c = cs[0], sn = cs[1];
+                        const float partner = s[0][r][tt][e ^ 1];  // rows 2i, 2i+1 share the lane
+                        const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
+                        if (row < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
+                        else a.out1[(size_t)local * a.max_seq + pos] = v;
+                    } else {
+                        a.out2[(size_t)pos * a.kvd + (row - a.seg2)] = y;
+                    }
                 }
             }
         }
-    }
 }
+
+// Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
+// token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
+// more leave too few waves to cover the latency at P = 512.
+enum { PF_NR = 2, PF_TW = 4, PF_PD = 2 };
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
-    const dim3 grid((a->P + 127) / 128, (a->rows + 63) / 64);  // token groups past P are not launched
+    if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
+    if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    if (a->epi == QMH_PF_SWIGLU) {
-        if (!a->il) return (int)hipErrorInvalidValue;
-        const dim3 g2((a->P + 63) / 64, (a->rows + 63) / 64);
-        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
-        else if (a->dtype == QMH_Q8) hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 4, 2>), g2, dim3(QMH_WG), 0, s, *a);
-        else return (int)hipErrorInvalidValue;
+    // token groups past P are not launched; 16 * PF_TW divides PP, so every B load stays in the
+    // PP-token activation buffer
+    const dim3 g((a->P + 16 * PF_TW - 1) / (16 * PF_TW), (a->rows + 64 * PF_NR - 1) / (64 * PF_NR));
+    if (a->il) {
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 2, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 2, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
     } else {
-        if (a->il) return (int)hipErrorInvalidValue;
-        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 8, 1>), grid, dim3(QMH_WG), 0, s, *a);
-        else if (a->dtype == QMH_Q8) hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 8, 1>), grid, dim3(QMH_WG), 0, s, *a);
-        else return (int)hipErrorInvalidValue;
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 1, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 1, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
     }
     return (int)hipGetLastError();
 }
