@@ -62,9 +62,10 @@ typedef struct {
 /* nslots: slots the codes/scales allocation holds; slots at or past it are never written */
 int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, int dtype, uint8_t *codes, uint16_t *scales,
                       int tile_r, int64_t row_off, int interleave_half, int64_t nslots, void *stream);
-int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream);
-/* dynamic LDS bytes the quantized matvec needs (must be <= 64 KiB) */
-size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm);
+/* quantized matvec (k_matvec): grid from qmh_matvec_grid (want: workgroups wanted, about one
+ * per CU; returns -1 if one tile does not fit the workgroup's LDS) */
+int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int want);
+int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream);
 /* longest row the quantized matvec takes, with (norm = 1) or without the RMSNorm prologue */
 int qmh_matvec_max_cols(int norm);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */

@@ -111,9 +111,19 @@ __device__ __forceinline__ void act_load(const qmh_mv_args &a, float4 *xr, float
     }
 }
 
+// Where the quantized blocks go in LDS: block b's codes at codes + r*cs, its d and code sum at
+// d[r*ds], sum[r*ds], for every record r = b, b + nb, b + 2nb, ... below nrec.
+struct ActDst {
+    int8_t *codes;
+    int cs;
+    float *d;
+    int *sum;
+    int ds, nrec;
+};
+
 template <bool SPLIT, bool NORM>
-__device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 *wr, int8_t *acodes, float *ad,
-                           int *asum, double *red) {
+__device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 *wr, const ActDst &dst,
+                           double *red) {
     constexpr int P = ActRegs<NORM>::P;
     const int n = a.cols, nb = a.nb, tid = threadIdx.x, sub = tid & 7;
     float inv = 1.0f;
@@ -171,17 +181,19 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
         qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
         const int ps = qmh_sum8(q[0] + q[1] + q[2] + q[3]);
         if (on) {
-            int8_t *c = acodes + b * 32;
-            if (SPLIT) {
-                *(uint16_t *)(c + sub * 2) = (uint16_t)((q[0] & 0xff) | ((q[2] & 0xff) << 8));
-                *(uint16_t *)(c + 16 + sub * 2) = (uint16_t)((q[1] & 0xff) | ((q[3] & 0xff) << 8));
-            } else {
-                *(uint32_t *)(c + sub * 4) = (uint32_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) |
-                                                        ((uint32_t)(q[3] & 0xff) << 24));
-            }
-            if (sub == 0) {
-                ad[b] = dd;
-                asum[b] = ps;
+            for (int rb = b; rb < dst.nrec; rb += nb) {
+                int8_t *c = dst.codes + rb * dst.cs;
+                if (SPLIT) {
+                    *(uint16_t *)(c + sub * 2) = (uint16_t)((q[0] & 0xff) | ((q[2] & 0xff) << 8));
+                    *(uint16_t *)(c + 16 + sub * 2) = (uint16_t)((q[1] & 0xff) | ((q[3] & 0xff) << 8));
+                } else {
+                    *(uint32_t *)(c + sub * 4) = (uint32_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8) |
+                                                            ((q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));
+                }
+                if (sub == 0) {
+                    dst.d[rb * dst.ds] = dd;
+                    dst.sum[rb * dst.ds] = ps;
+                }
             }
             if (a.xq_out && blockIdx.x == 0) {
                 uint8_t *o = a.xq_out + (size_t)b * 34;
@@ -296,90 +308,75 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
     }
 }
 
-// The serial chain of one row: s = +0; s = s + t[b] for b = 0..nb-1. The row is read as
-// chunks of 32 floats (8 float4) with the next chunk in flight while the current one is added;
-// rows are zero from nb to a whole chunk (adding +0 to a sum that started at +0 changes
-// nothing: such a sum is never -0), so the loop has no conditions.
-__device__ __forceinline__ float mv_chain(const float *row, int nb) {
-    const float4 *r4 = (const float4 *)row;
-    const int nc = (nb + 31) >> 5;
-    float s = 0.0f;
-    float4 v[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) v[k] = r4[k];
-    for (int c = 0; c < nc; c++) {
-        const int nx = c + 1 < nc ? c + 1 : c;
-        float4 w[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) w[k] = r4[nx * 8 + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            s = s + v[k].x;
-            s = s + v[k].y;
-            s = s + v[k].z;
-            s = s + v[k].w;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = w[k];
-    }
-    return s;
-}
+// activation modes of k_matvec: quantize x (optionally RMSNorm'd first), or copy a quantized
+// image another kernel wrote (QMH_XQ_IMAGE_BYTES layout)
+enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
+constexpr int MV_IMAGE_REGS = 4;  // uint4 per thread: images up to 16 KiB (nb <= 409)
+
+#ifndef QMH_MV_D
+#define QMH_MV_D 2  // chunks in flight per workgroup
+#endif
+#ifndef QMH_MV_CH
+#define QMH_MV_CH 4  // Q4_0 slots per thread per chunk (Q8_0: half)
+#endif
 
 // ============================================================================ quantized matvec
 //
 // y = W x with W Q4_0 or Q8_0 and x quantized to Q8_0 (src/ops.c:36-61), one row's dot as in
 // src/kernels_scalar.c:12-34:  s = +0; for b: s = s + (float)acc_b * (d_w,b * d_x,b).
+// acc_b, the int32 dot of one block, is exact in any order (sdot4); the float steps keep the
+// reference's order: each term t_b = (float)acc_b * (d_w*d_x) is rounded as the reference
+// rounds it, and each row's terms are summed by one lane in block order.
 //
-// Workgroup = 256 threads, grid-stride over tiles of R rows, tile = R*nb blocks cut into
-// chunks of 256*CH blocks (thread tid owns blocks l = chunk*256*CH + k*256 + tid). Per chunk:
-//   1. the NEXT chunk's code/scale loads are issued first (two register buffers used
-//      alternately; the allocation is padded so these loads are unconditional and the
-//      compiler waits for exactly the older chunk),
-//   2. the exact int32 block dot against the LDS activation and the term
-//      t = (float)acc * (d_w*d_x) go to T[r][b] in LDS,
-//   3. after the tile's last chunk, lanes 0..R-1 run each row's serial chain, then the
-//      epilogue.
+// Layout of the work, for bandwidth and few instructions per block:
+//   * about one workgroup per CU, each owning a contiguous range of whole tiles (contiguous
+//     slots), streamed as chunks of 256*CH slots through a ring of D register buffers: the
+//     activation prologue runs under the first D chunks, and only the range's last chunk is
+//     partial;
+//   * buffer loads with a per-lane byte offset fixed for the whole kernel; each load's
+//     resource starts at its 256 slots (scalar arithmetic), and the hardware range check
+//     zeroes slots past the range without a memory access;
+//   * the activation in LDS as 48-byte records (32 codes, d, code sum), laid out unrolled:
+//     record j holds block j mod nb for j < nb + CHUNK/R, so a chunk's records are a scalar
+//     base plus a per-lane constant and nothing wraps;
+//   * the terms in LDS in slot order (T[l] for the range's slot l), so the store address is a
+//     per-lane constant plus the chunk's base. After the last chunk every row's serial chain
+//     walks its terms (stride R), then the epilogue.
+// Each workgroup quantizes the activation once for all of its rows.
+constexpr int MV_REC = 48;  // LDS bytes per activation record
 
-// LDS row stride of T: >= nb rounded up to whole 32-float chunks (the chain reads them), and
-// == 4 mod 64 floats so the chain lanes' float4 reads and the compute phase's writes fall in
-// distinct banks
-__host__ __device__ __forceinline__ int mv_tstride(int nb) {
-    const int n32 = (nb + 31) & ~31;
-    return n32 + (((4 - n32) % 64) + 64) % 64;
+__host__ __device__ __forceinline__ int mv_tile0(int w, int ntiles, int G) {
+    return (int)((long long)w * ntiles / G);
+}
+__host__ __device__ __forceinline__ int mv_nrec(int nb, int R, int chq4, int dtype_q4) {
+    return nb + QMH_WG * (dtype_q4 ? chq4 : chq4 / 2) / R;
+}
+// dynamic LDS bytes of k_matvec: the records, then T for up to `tiles` tiles
+__host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, int tiles, int chq4, int dtype_q4) {
+    return (size_t)mv_nrec(nb, R, chq4, dtype_q4) * MV_REC + 4 * (size_t)tiles * R * nb;
 }
 
-// dynamic LDS bytes of k_matvec for (nb, R): the activation image (codes, scales, code sums;
-// QMH_XQ_IMAGE_BYTES), then T
-__host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, bool norm) {
-    (void)norm;
-    return QMH_XQ_IMAGE_BYTES(nb) + 4 * (size_t)R * mv_tstride(nb);
-}
+typedef unsigned int mv_u32x4 __attribute__((ext_vector_type(4)));
 
-// activation modes of k_matvec
-enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
-constexpr int MV_IMAGE_REGS = 4;  // uint4 per thread: images up to 16 KiB (nb <= 409)
-
-template <int WT, int R, int AM>
+template <int WT, int R, int AM, int D, int CHQ4>
 __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     constexpr bool NORM = AM == MV_ACT_NORM;
-    constexpr int CB = WT == QMH_Q4 ? 16 : 32;  // code bytes per block
-    constexpr int NV = CB / 16;                 // uint4 per block
-    constexpr int CH = WT == QMH_Q4 ? 8 : 4;    // blocks per thread per chunk
+    constexpr int CB = WT == QMH_Q4 ? 16 : 32;           // code bytes per block
+    constexpr int NV = CB / 16;                          // uint4 per block
+    constexpr int CH = WT == QMH_Q4 ? CHQ4 : CHQ4 / 2;   // slots per thread per chunk
     constexpr int CHUNK = QMH_WG * CH;
+    static_assert(QMH_WG % R == 0 && CHUNK % R == 0, "a chunk holds whole block columns");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
 
-    const int nb = a.nb, TB = R * nb, nchunk = (TB + CHUNK - 1) / CHUNK, S = mv_tstride(nb);
-    const int tid = threadIdx.x;
-    int tile = blockIdx.x;
-    if (tile >= a.ntiles) return;
+    const int nb = a.nb, TB = R * nb, tid = threadIdx.x;
+    const int t0 = mv_tile0(blockIdx.x, a.ntiles, gridDim.x), t1 = mv_tile0(blockIdx.x + 1, a.ntiles, gridDim.x);
+    const int ntw = t1 - t0, nslot = ntw * TB, nch = (nslot + CHUNK - 1) / CHUNK;
+    if (ntw <= 0) return;  // the host launches at most ntiles workgroups
+    const int nrec = nb + CHUNK / R;
+    float *T = (float *)(smem + (size_t)nrec * MV_REC);
 
-    int8_t *acodes = (int8_t *)smem;
-    float *ad = (float *)(smem + (size_t)nb * 32);
-    int *asum = (int *)(smem + (size_t)nb * 36);
-    float *T = (float *)(smem + QMH_XQ_IMAGE_BYTES(nb));  // [R][S] per-block terms
-
-    // 1. activation (and gain) loads, or the quantized image's
+    // 1. activation (or image) loads, issued first so waiting for them never waits for weights
     float4 xr[AM == MV_ACT_IMAGE ? 1 : ActRegs<NORM>::P], wr[NORM ? ActRegs<NORM>::P : 1];
     uint4 im[AM == MV_ACT_IMAGE ? MV_IMAGE_REGS : 1];
     const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
@@ -396,110 +393,150 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
 
-    const uint4 *codes = (const uint4 *)a.codes;
-    uint4 A[CH][NV], B[CH][NV];
-    uint32_t As[CH], Bs[CH];
+    // 2. the first D chunks. Each load's resource starts at its own 256 slots and holds what is
+    // left of the range, so the range check (on the lane's offset) zeroes slots past the range
+    // without touching memory; the resources are scalar arithmetic.
+    const uint8_t *cbase = (const uint8_t *)a.codes + (size_t)t0 * TB * CB;
+    const uint8_t *sbase = (const uint8_t *)(a.scales + (size_t)t0 * TB);
+    mv_u32x4 C[D][CH][NV];
+    uint32_t Sc[D][CH];
+#define MV_LOAD(J, CHK)                                                                          \
+    _Pragma("unroll") for (int k = 0; k < CH; k++) {                                              \
+        const int so = (CHK) * CHUNK + k * QMH_WG, left = nslot - so > 0 ? nslot - so : 0;        \
+        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(                      \
+            (void *)(cbase + (size_t)so * CB), (short)0, left * CB, 0x00020000);                  \
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
+            (void *)(sbase + (size_t)so * 2), (short)0, left * 2, 0x00020000);                    \
+        _Pragma("unroll") for (int v = 0; v < NV; v++) C[J][k][v] =                               \
+            __builtin_amdgcn_raw_buffer_load_b128(rc, tid * CB + 16 * v, 0, 0);                   \
+        Sc[J][k] = __builtin_amdgcn_raw_buffer_load_b16(rs, tid * 2, 0, 0);                       \
+    }
+#pragma unroll
+    for (int j = 0; j < D; j++) MV_LOAD(j, j);
 
-    // lanes past the tile's last block re-read the tile's first block (already in cache)
-    // instead of the next tile, so the unconditional loads add no memory traffic
-#define QMH_LOAD(BUF, BS, TILE, CHK)                                                           \
-    {                                                                                          \
-        const size_t tbase = (size_t)(TILE) * TB;                                              \
-        _Pragma("unroll") for (int k = 0; k < CH; k++) {                                       \
-            const int l = (CHK) * CHUNK + k * QMH_WG + tid;                                    \
-            const size_t slot = tbase + (size_t)(l < TB ? l : 0);                              \
-            _Pragma("unroll") for (int v = 0; v < NV; v++) BUF[k][v] = codes[slot * NV + v];   \
-            BS[k] = a.scales[slot];                                                            \
-        }                                                                                      \
+    // the first row group's epilogue inputs, while the weights stream
+    const int rows_w = ntw * R;
+    EpiIn ein = {0.0f, 1.0f, 0.0f};
+    if (tid < rows_w) {
+        const int tile = t0 + tid / R, r = tid % R;
+        ein = epi_fetch(a, R >= 2 * QMH_TILE_R ? tile * (R / 2) + (r & (R / 2 - 1)) : tile * R + r, pos);
     }
 
-#define QMH_COMPUTE(BUF, BS, CHK)                                                                        \
-    _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
-        const int l = (CHK) * CHUNK + k * QMH_WG + tid;                                                  \
-        if (l < TB) {                                                                                    \
-            const int b = l / R, r = l % R;                                                              \
-            const int4 *xv = (const int4 *)(acodes + b * 32);                                            \
-            const int4 x0 = xv[0], x1 = xv[1];                                                           \
-            int acc = 0;                                                                                 \
-            if (WT == QMH_Q4) {                                                                          \
-                const uint4 w = BUF[k][0];                                                               \
-                acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);                \
-                acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);         \
-                acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);                \
-                acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);         \
-                acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);                \
-                acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);         \
-                acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);                \
-                acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);         \
-                acc -= 8 * asum[b]; /* sum (q-8)*x = sum q*x - 8*sum x, exact */                         \
-            } else {                                                                                     \
-                const uint4 w0 = BUF[k][0], w1 = BUF[k][NV - 1];                                         \
-                acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);                               \
-                acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);                               \
-            }                                                                                            \
-            T[r * S + b] = (float)acc * (qmh_h2f((uint16_t)BS[k]) * ad[b]);                              \
-        }                                                                                                \
-    }
-
-    // one step: epilogue inputs (tile's last chunk only), then the loads of the chunk after
-    // (tile, c) into NXT, then compute CUR and finish the tile. When nothing follows, NXT
-    // re-reads the current chunk (an L2 hit) so the loads stay unconditional.
-#define QMH_STEP(CUR, CURS, NXT, NXTS)                                                         \
-    {                                                                                          \
-        int nt = tile, nc = c + 1;                                                             \
-        if (nc == nchunk) {                                                                    \
-            nt = tile + gridDim.x;                                                             \
-            nc = 0;                                                                            \
-        }                                                                                      \
-        more = nt < a.ntiles;                                                                  \
-        const int row = R >= 2 * QMH_TILE_R ? tile * (R / 2) + (tid & (R / 2 - 1))             \
-                                            : tile * R + (tid & (R - 1));                      \
-        EpiIn ein = {0.0f, 1.0f, 0.0f};                                                        \
-        if (c == nchunk - 1) ein = epi_fetch(a, row, pos);                                     \
-        QMH_LOAD(NXT, NXTS, more ? nt : tile, more ? nc : c);                                  \
-        QMH_COMPUTE(CUR, CURS, c);                                                             \
-        if (c == nchunk - 1) {                                                                 \
-            __syncthreads();                                                                   \
-            if (tid < R) mv_epilogue<R>(a, row, mv_chain(T + tid * S, nb), tid, pos, ein);        \
-            __syncthreads();                                                                   \
-        }                                                                                      \
-        tile = nt;                                                                             \
-        c = nc;                                                                                \
-    }
-
-    // 2. first weight chunk, then 3. the activation into LDS while it is in flight
-    QMH_LOAD(A, As, tile, 0);
-    // zero T once (the chain adds whole float4s, the pad past nb must read +0); the
-    // prologue's closing barrier publishes it
-    for (int i = tid; i < R * S; i += QMH_WG) T[i] = 0.0f;
+    // 3. the activation records
     if (AM == MV_ACT_IMAGE) {
+        // global image: codes [nb][32], then d [nb], then code sums [nb] (QMH_XQ_IMAGE_BYTES)
 #pragma unroll
         for (int k = 0; k < MV_IMAGE_REGS; k++) {
             const int i = k * QMH_WG + tid;
-            if (k * QMH_WG < nimg && i < nimg) ((uint4 *)smem)[i] = im[k];
+            if (k * QMH_WG < nimg && i < nimg) {
+                const int o = 16 * i;
+                if (o < nb * 32) {
+                    for (int rb = o / 32; rb < nrec; rb += nb)
+                        *(uint4 *)(smem + rb * MV_REC + (o & 31)) = im[k];
+                } else {
+                    const uint32_t w4[4] = {im[k].x, im[k].y, im[k].z, im[k].w};
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+                        const int ow = o + 4 * w;
+                        const int isd = ow < nb * 36, b = isd ? (ow - nb * 32) / 4 : (ow - nb * 36) / 4;
+                        if (ow < nb * 40)
+                            for (int rb = b; rb < nrec; rb += nb)
+                                *(uint32_t *)(smem + rb * MV_REC + (isd ? 32 : 36)) = w4[w];
+                    }
+                }
+            }
         }
         __syncthreads();
     } else {
-        act_finish<WT == QMH_Q4, NORM>(a, xr, wr, acodes, ad, asum, red);
+        act_finish<WT == QMH_Q4, NORM>(a, xr, wr,
+                                       ActDst{(int8_t *)smem, MV_REC, (float *)(smem + 32), (int *)(smem + 36),
+                                              MV_REC / 4, nrec},
+                                       red);
     }
 
-    int c = 0;
-    bool more = true;
-    for (;;) {
-        QMH_STEP(A, As, B, Bs);
-        if (!more) break;
-        QMH_STEP(B, Bs, A, As);
-        if (!more) break;
+    // 4. the stream. Thread tid's slot k of chunk c is l = c*CHUNK + k*256 + tid: block
+    // column (l / R) = c*CHUNK/R + k*256/R + tid/R, record (that mod nb) = um + k*256/R + tid/R
+    // with um = (c*CHUNK/R) mod nb.
+    const uint8_t *rec_t = smem + (tid / R) * MV_REC;
+    float *T_t = T + tid;
+#define MV_COMPUTE(J, CHK, UM, CHECK)                                                                   \
+    _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
+        const uint8_t *rp = rec_t + ((UM) + k * (QMH_WG / R)) * MV_REC;                                 \
+        const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);                                \
+        const float2 ds = *(const float2 *)(rp + 32);                                                    \
+        int acc;                                                                                         \
+        if (WT == QMH_Q4) {                                                                              \
+            const mv_u32x4 w = C[J][k][0];                                                              \
+            acc = -8 * __float_as_int(ds.y); /* sum (q-8)*x = sum q*x - 8*sum x, exact */                \
+            acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);                    \
+            acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);             \
+            acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);                    \
+            acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);             \
+            acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);                    \
+            acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);             \
+            acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);                    \
+            acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);             \
+        } else {                                                                                         \
+            const mv_u32x4 w0 = C[J][k][0], w1 = C[J][k][NV - 1];                                       \
+            acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, 0, false);                                     \
+            acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);                                   \
+            acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);                                   \
+        }                                                                                                \
+        const float t = (float)acc * (qmh_h2f((uint16_t)Sc[J][k]) * ds.x);                               \
+        if (!(CHECK) || (CHK) * CHUNK + k * QMH_WG + tid < nslot) T_t[(CHK) * CHUNK + k * QMH_WG] = t;  \
     }
-#undef QMH_STEP
-#undef QMH_COMPUTE
-#undef QMH_LOAD
+
+    int c0 = 0, um = 0;  // um: record of the chunk's first block column
+    const int ustep = CHUNK / R % nb;
+    for (; c0 + D < nch; c0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            MV_COMPUTE(j, c0 + j, um, false);
+            MV_LOAD(j, c0 + j + D);
+            um += ustep;
+            um -= um >= nb ? nb : 0;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < D; j++)
+        if (c0 + j < nch) {
+            MV_COMPUTE(j, c0 + j, um, true);
+            um += ustep;
+            um -= um >= nb ? nb : 0;
+        }
+#undef MV_COMPUTE
+#undef MV_LOAD
+    __syncthreads();
+
+    // 5. serial chains (row i of the range: tile i/R, row i%R; its terms at (tile*nb + b)*R + i%R)
+    // and epilogues; a wave holds whole tiles (R divides 64, or R == 64)
+    for (int i0 = 0; i0 < rows_w; i0 += QMH_WG) {
+        const int i = i0 + tid;
+        if (i0 + (tid & ~63) >= rows_w) break;  // the whole wave is past the range
+        const int tl = i / R, r = i % R, tile = t0 + tl;
+        const int row = R >= 2 * QMH_TILE_R ? tile * (R / 2) + (r & (R / 2 - 1)) : tile * R + r;
+        const bool mine = i < rows_w;
+        if (i0 > 0 && mine) ein = epi_fetch(a, row, pos);
+        float y = 0.0f;
+        if (mine) {
+            const float *tp = T + (size_t)tl * TB + r;
+            int b = 0;
+            for (; b + 32 <= nb; b += 32) {
+                float v[32];
+#pragma unroll
+                for (int k = 0; k < 32; k++) v[k] = tp[(b + k) * R];
+#pragma unroll
+                for (int k = 0; k < 32; k++) y = y + v[k];
+            }
+            for (; b < nb; b++) y = y + tp[b * R];
+        }
+        mv_epilogue<R>(a, mine ? row : a.rows, y, r, pos, ein);
+    }
 }
 
 // f32 weights (src/kernels_scalar.c:6-10 via src/ops.c:42-45): lane per row, x in LDS,
@@ -540,47 +577,55 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
     mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e);
 }
 
-extern "C" size_t qmh_matvec_lds_bytes(int nb, int tile_r, int norm) { return mv_lds_bytes(nb, tile_r, norm != 0); }
-
 extern "C" int qmh_matvec_max_cols(int norm) { return (norm ? ActRegs<true>::P : ActRegs<false>::P) * QMH_WG * 4; }
 
-extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid_cap, void *stream) {
-    const int grid = a->ntiles < grid_cap ? a->ntiles : grid_cap;
+// Workgroups for k_matvec: `want` (about one per CU; more for matrices of many tiles), never
+// more than ntiles, and enough that a workgroup's records and terms fit the 64 KiB of LDS one
+// workgroup may take. -1: one tile does not fit.
+extern "C" int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int want) {
+    if (ntiles < 1 || nb < 1 || (dtype != QMH_Q4 && dtype != QMH_Q8)) return -1;
+    const size_t rec = (size_t)mv_nrec(nb, tile_r, QMH_MV_CH, dtype == QMH_Q4) * MV_REC, per = 4 * (size_t)tile_r * nb;
+    if (rec + per > 65536) return -1;
+    const int maxt = (int)((65536 - rec) / per);
+    int g = want < ntiles ? want : ntiles;
+    const int need = (ntiles + maxt - 1) / maxt;
+    return g > need ? g : need;
+}
+
+extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     const bool norm = a->norm_w != NULL, image = a->xq_in != NULL;
-    const size_t lds = mv_lds_bytes(a->nb, a->tile_r, norm);
-    if (lds > 65536 || a->cols > qmh_matvec_max_cols(norm) || a->cols < 1 || (norm && image)) return (int)hipErrorInvalidValue;
+    if (grid < 1 || grid > a->ntiles || a->cols < 1 || a->cols > qmh_matvec_max_cols(norm) || (norm && image))
+        return (int)hipErrorInvalidValue;
+    if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
+    const int tmax = (a->ntiles + grid - 1) / grid;
+    const size_t lds = mv_lds_bytes(a->nb, a->tile_r, tmax, QMH_MV_CH, a->dtype == QMH_Q4);
+    if (lds > 65536 || (long long)tmax * a->tile_r * a->nb * (a->dtype == QMH_Q4 ? 16 : 32) >= (1ll << 31))
+        return (int)hipErrorInvalidValue;
     if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)MV_IMAGE_REGS * QMH_WG * 16) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_EPI_SWIGLU_Q) != (a->tile_r == 64)) return (int)hipErrorInvalidValue;
     const int am = image ? MV_ACT_IMAGE : norm ? MV_ACT_NORM : MV_ACT;
     hipStream_t s = (hipStream_t)stream;
-#define QMH_MV(WT, R, AM) hipLaunchKernelGGL((k_matvec<WT, R, AM>), dim3(grid), dim3(QMH_WG), lds, s, *a)
-#define QMH_MV_R(WT)                                                                    \
-    if (a->tile_r == 8 || a->tile_r == 16) {                                            \
-        if (am == MV_ACT_NORM) {                                                        \
-            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT_NORM); else QMH_MV(WT, 16, MV_ACT_NORM); \
-        } else if (am == MV_ACT_IMAGE) {                                                \
-            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT_IMAGE); else QMH_MV(WT, 16, MV_ACT_IMAGE); \
-        } else {                                                                        \
-            if (a->tile_r == 8) QMH_MV(WT, 8, MV_ACT); else QMH_MV(WT, 16, MV_ACT);     \
-        }                                                                               \
-    } else if (a->tile_r == 32) {                                                       \
-        if (am == MV_ACT_NORM) QMH_MV(WT, 32, MV_ACT_NORM); else if (am == MV_ACT) QMH_MV(WT, 32, MV_ACT); \
-        else return (int)hipErrorInvalidValue;                                          \
-    } else if (a->tile_r == 64) {                                                       \
-        if (am == MV_ACT_NORM) QMH_MV(WT, 64, MV_ACT_NORM); else if (am == MV_ACT) QMH_MV(WT, 64, MV_ACT); \
-        else return (int)hipErrorInvalidValue;                                          \
-    } else {                                                                            \
-        return (int)hipErrorInvalidValue;                                               \
+#define QMH_MV(WT, R, AM) hipLaunchKernelGGL((k_matvec<WT, R, AM, QMH_MV_D, QMH_MV_CH>), dim3(grid), dim3(QMH_WG), lds, s, *a)
+#define QMH_MV_AM(WT, R)                                                  \
+    if (am == MV_ACT_NORM) QMH_MV(WT, R, MV_ACT_NORM);                    \
+    else if (am == MV_ACT_IMAGE) QMH_MV(WT, R, MV_ACT_IMAGE);             \
+    else QMH_MV(WT, R, MV_ACT);
+#define QMH_MV_R(WT)                                                      \
+    switch (a->tile_r) {                                                   \
+    case 8: QMH_MV_AM(WT, 8); break;                                      \
+    case 16: QMH_MV_AM(WT, 16); break;                                    \
+    case 32: QMH_MV_AM(WT, 32); break;                                    \
+    case 64: QMH_MV_AM(WT, 64); break;                                    \
+    default: return (int)hipErrorInvalidValue;                             \
     }
     if (a->dtype == QMH_Q4) {
         QMH_MV_R(QMH_Q4);
-    } else if (a->dtype == QMH_Q8) {
-        QMH_MV_R(QMH_Q8);
     } else {
-        return (int)hipErrorInvalidValue;
+        QMH_MV_R(QMH_Q8);
     }
 #undef QMH_MV_R
-#undef QMH_MV
+#undef QMH_MV_AM
+#undef QMH_MVS
     return (int)hipGetLastError();
 }
 

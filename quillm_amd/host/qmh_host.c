@@ -49,7 +49,7 @@ const char *qmh_last_error(void) { return g_err; }
 
 /* ------------------------------------------------------------------ runtime */
 
-static int g_ready, g_dev = -1, g_cus = 256, g_mv_grid = 512;
+static int g_ready, g_dev = -1, g_cus = 256;
 static hipStream_t g_stream;
 static float *g_rope_scratch; /* op-level rope: one position's (cos, sin) pairs */
 #define ROPE_SCRATCH_PAIRS 4096
@@ -77,9 +77,6 @@ int qmh_init(int device) {
     HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     HIPCHK(hipMalloc((void **)&g_rope_scratch, sizeof(float) * 2 * ROPE_SCRATCH_PAIRS));
     g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
-    /* tuning knob: workgroups of the quantized matvec (default 3 per CU: the occupancy its registers allow) */
-    const char *gv = getenv("QMH_MV_GRID");
-    g_mv_grid = gv && atoi(gv) > 0 ? atoi(gv) : 3 * g_cus;
     g_dev = device;
     g_ready = 1;
     return 0;
@@ -323,10 +320,13 @@ static void mv_args_for(const struct qmh_weight *w, qmh_mv_args *a) {
     a->rows = (int)w->rows;
 }
 
-static int mv_grid_cap(void) { return g_mv_grid; }
-
+/* one workgroup per CU; four per CU for matrices of many tiles (the output matrix), whose
+ * workgroups would otherwise each stream a long range behind a short prologue */
 static int mv_launch(const qmh_mv_args *a, hipStream_t s) {
-    return a->dtype == QMH_F32 ? qmh_launch_matvec_f32(a, s) : qmh_launch_matvec(a, mv_grid_cap(), s);
+    if (a->dtype == QMH_F32) return qmh_launch_matvec_f32(a, s);
+    const int want = g_cus * (a->ntiles >= 6 * g_cus ? 4 : 1);
+    const int grid = qmh_matvec_grid(a->ntiles, a->nb, a->tile_r, a->dtype, want);
+    return grid < 1 ? (int)hipErrorInvalidValue : qmh_launch_matvec(a, grid, s);
 }
 
 int qmh_matvec(const qmh_weight *W, const float *x, float *y, void *xq, void *stream) {
@@ -644,8 +644,9 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     }
     /* LDS budget of the kernels (64 KiB per workgroup) */
     const int nbD = (int)((D + 31) / 32), nbH = (int)((H + 31) / 32);
-    if (qmh_matvec_lds_bytes(nbD, 64, 1) > 65536 || qmh_matvec_lds_bytes(nbD, QMH_TILE_R, 1) > 65536 ||
-        qmh_matvec_lds_bytes(nbH, QMH_TILE_R, 0) > 65536 || D > qmh_matvec_max_cols(1) || H > qmh_matvec_max_cols(0))
+    if (qmh_matvec_grid(1, nbD, 64, QMH_Q4_0, 1) < 1 || qmh_matvec_grid(1, nbD, QMH_TILE_R, QMH_Q4_0, 1) < 1 ||
+        qmh_matvec_grid(1, nbD, 8, QMH_Q4_0, 1) < 1 || qmh_matvec_grid(1, nbH, 8, QMH_Q4_0, 1) < 1 ||
+        D > qmh_matvec_max_cols(1) || H > qmh_matvec_max_cols(0))
         return fail("model dims exceed the kernels' limits (dim <= %d, hidden_dim <= %d)", qmh_matvec_max_cols(1),
                     qmh_matvec_max_cols(0));
     if (((int64_t)64 * (m->hd + 1) + (int64_t)m->group * m->hd) * 4 > 65536 || m->group > 15)
