@@ -77,21 +77,41 @@ extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float
 
 // ============================================================================ softmax + V sum
 
-#define QMH_PV_CW 16   // output columns per workgroup
-#define QMH_PV_TC 256  // positions per LDS chunk
-#define QMH_PV_VS (QMH_PV_TC + 4)  // LDS row stride of the V chunk (== 4 mod 64 floats)
+#define QMH_PV_CW 16  // output columns per workgroup
 
+// TC: positions per LDS chunk. 640 when the LDS holds it (group <= 8): a context of up to 640
+// positions is then one chunk, every V value of the workgroup requested at once.
+template <int TC>
 __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ att, const float *__restrict__ V,
                                                     float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
                                                     int n_kv, int hd, int max_seq) {
-    __shared__ __align__(16) float P[16 * QMH_PV_TC];          // [group][TC] probabilities
-    __shared__ __align__(16) float Vs[QMH_PV_CW * QMH_PV_VS];  // [CW][TC] the chunk, transposed
+    constexpr int QMH_PV_TC = TC, QMH_PV_VS = TC + 4;  // V chunk row stride == 4 mod 64 floats
+    static_assert(TC % 32 == 0 && TC * QMH_PV_CW % QMH_WG == 0, "whole 32-position steps, whole loads");
+    extern __shared__ __align__(16) float pv_smem[];
+    float *P = pv_smem;                              // [group][TC] probabilities
+    float *Vs = pv_smem + (n_heads / n_kv) * TC;     // [CW][TC] the chunk, transposed
     __shared__ double red[16];
     __shared__ float redf[16];
     __shared__ float mx_s[16], inv_s[16];
     const int n = *pos_ptr + 1;
     if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
     const int kvh = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, group = n_heads / n_kv, kvd = hd * n_kv;
+    const int lane_h = threadIdx.x / QMH_PV_CW, col = threadIdx.x % QMH_PV_CW;
+    const bool chain = lane_h < group;
+    const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
+    constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
+    float acc = 0.0f;
+    // a chunk's V values: unconditional, clamped loads, all in flight together (the first
+    // chunk's under the softmax statistics); the next chunk's are issued before the current
+    // chunk's chain runs
+    float vv[LPT];
+#define QMH_PV_LOAD(T0)                                                 \
+    _Pragma("unroll") for (int k = 0; k < LPT; k++) {                   \
+        const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW;      \
+        const int tcl = (T0) + t < n ? (T0) + t : n - 1;                \
+        vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];                 \
+    }
+    QMH_PV_LOAD(0);
     // softmax statistics per head of the group (src/ops.c:100-112)
     for (int hl = 0; hl < group; hl++) {
         const float *s = att + (size_t)(kvh * group + hl) * max_seq;
@@ -122,21 +142,6 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
         }
     }
     __syncthreads();
-    const int lane_h = threadIdx.x / QMH_PV_CW, col = threadIdx.x % QMH_PV_CW;
-    const bool chain = lane_h < group;
-    const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
-    constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
-    float acc = 0.0f;
-    // a chunk's V values: unconditional, clamped loads, all in flight together; the next
-    // chunk's are issued before the current chunk's chain runs
-    float vv[LPT];
-#define QMH_PV_LOAD(T0)                                                 \
-    _Pragma("unroll") for (int k = 0; k < LPT; k++) {                   \
-        const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW;      \
-        const int tcl = (T0) + t < n ? (T0) + t : n - 1;                \
-        vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];                 \
-    }
-    QMH_PV_LOAD(0);
     for (int t0 = 0; t0 < n; t0 += QMH_PV_TC) {
         const int nt = min(QMH_PV_TC, n - t0);
         // probabilities of the chunk, +0 past nt
@@ -156,14 +161,36 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
         if (chain) {
             // out = out + p_t*v_t in t order; the chunk is zero past nt (p*0 = +0 and the sum,
             // which started at +0, is never -0, so the extra terms change nothing)
+            // 32 positions per step, the next step's LDS reads in flight during this step's adds
+            // (TC is a multiple of 32 and the chunk is zero up to TC)
             const float4 *p4 = (const float4 *)(P + lane_h * QMH_PV_TC), *v4 = (const float4 *)(Vs + col * QMH_PV_VS);
-            const int n4 = (nt + 3) >> 2;
-            for (int k = 0; k < n4; k++) {
-                const float4 p = p4[k], v = v4[k];
-                acc = acc + p.x * v.x;
-                acc = acc + p.y * v.y;
-                acc = acc + p.z * v.z;
-                acc = acc + p.w * v.w;
+            const int n32 = (nt + 31) >> 5;
+            float4 pc[8], vc[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                pc[j] = p4[j];
+                vc[j] = v4[j];
+            }
+            for (int k = 0; k < n32; k++) {
+                float4 pn[8], vn[8];
+                const int kn = k + 1 < n32 ? k + 1 : k;  // the last step re-reads itself
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    pn[j] = p4[8 * kn + j];
+                    vn[j] = v4[8 * kn + j];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    acc = acc + pc[j].x * vc[j].x;
+                    acc = acc + pc[j].y * vc[j].y;
+                    acc = acc + pc[j].z * vc[j].z;
+                    acc = acc + pc[j].w * vc[j].w;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    pc[j] = pn[j];
+                    vc[j] = vn[j];
+                }
             }
         }
         __syncthreads();
@@ -177,7 +204,12 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *
     const int group = n_heads / n_kv_heads;
     if (group > 16 || group * QMH_PV_CW > QMH_WG) return (int)hipErrorInvalidValue;
     dim3 grid(n_kv_heads, (head_dim + QMH_PV_CW - 1) / QMH_PV_CW);
-    hipLaunchKernelGGL(k_attn_pv, grid, dim3(QMH_WG), 0, (hipStream_t)stream, att, vcache, out, pos_ptr, n_heads,
-                       n_kv_heads, head_dim, max_seq);
+    hipStream_t s = (hipStream_t)stream;
+#define QMH_PV_GO(TC)                                                                                     \
+    hipLaunchKernelGGL(k_attn_pv<TC>, grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
+                       s, att, vcache, out, pos_ptr, n_heads, n_kv_heads, head_dim, max_seq)
+    if (group <= 8) QMH_PV_GO(640);
+    else QMH_PV_GO(256);
+#undef QMH_PV_GO
     return (int)hipGetLastError();
 }
