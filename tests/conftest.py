@@ -54,6 +54,8 @@ SMALL_SHAPES = {
     "small": dict(dim=64, hidden_dim=172, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=458, max_seq=64),
     "odd": dict(dim=72, hidden_dim=200, n_layers=3, n_heads=6, n_kv_heads=3, vocab_size=458, max_seq=64),
     "mha": dict(dim=96, hidden_dim=256, n_layers=2, n_heads=3, n_kv_heads=3, vocab_size=300, max_seq=48),
+    # 12 query heads on one kv head, and a context past one 256-position attention chunk
+    "gqa": dict(dim=96, hidden_dim=256, n_layers=2, n_heads=12, n_kv_heads=1, vocab_size=300, max_seq=300),
 }
 
 

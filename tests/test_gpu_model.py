@@ -20,12 +20,13 @@ def say(*a):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("shape", ["small", "odd", "mha"])
+@pytest.mark.parametrize("shape", ["small", "odd", "mha", "gqa"])
 @pytest.mark.parametrize("wt", ["f32", "q8_0", "q4_0"])
 def test_forward_matches_oracle(gpu, oracle, small_models, shape, wt):
     path = small_models[(shape, wt)]
     say(f"case {shape}/{wt}: load {path}")
-    prompt = gpu.prompt_ids(6, 300 if shape == "mha" else 458, seed=5)
+    # gqa: 270 prompt tokens, so the attention context passes one 256-position chunk
+    prompt = gpu.prompt_ids(270 if shape == "gqa" else 6, 300 if shape in ("mha", "gqa") else 458, seed=5)
     want, want_ids = oracle.run_model(path, prompt, n_gen=20)
     with gpu.Model.load(path) as m:
         got = []

@@ -12,11 +12,11 @@ from _bind import F32, Q4_0, Q8_0, REF_CLI, ref_run, row_bytes
 DT = {"f32": F32, "q8_0": Q8_0, "q4_0": Q4_0}
 
 
-@pytest.mark.parametrize("shape", ["small", "odd", "mha"])
+@pytest.mark.parametrize("shape", ["small", "odd", "mha", "gqa"])
 @pytest.mark.parametrize("wt", ["f32", "q8_0", "q4_0"])
 def test_oracle_forward_bitexact_vs_reference(oracle, small_models, qmh, shape, wt):
     path = small_models[(shape, wt)]
-    prompt = qmh.prompt_ids(6, 300 if shape == "mha" else 458, seed=5)
+    prompt = qmh.prompt_ids(270 if shape == "gqa" else 6, 300 if shape in ("mha", "gqa") else 458, seed=5)
     lg, ids = oracle.run_model(path, prompt, n_gen=14)
     res, rl = ref_run(path, prompt, 14, isa="scalar")
     rl = rl.reshape(lg.shape)
