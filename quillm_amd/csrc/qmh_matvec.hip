@@ -73,35 +73,37 @@ extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, i
 //                     low/high nibbles; asum[b] = sum of the codes.
 //   ad[b]            : fp32(fp16(d)) of the block.
 
-template <bool NORM>
+// float4 of the activation per thread (passes) for NT threads: cols <= P*4*NT, at least 6144
+// with RMSNorm and 12288 without
+template <bool NORM, int NT>
 struct ActRegs {
-    static constexpr int P = NORM ? 6 : 12;  // float4 per thread (passes): cols <= P*1024
+    static constexpr int P = ((NORM ? 6144 : 12288) + 4 * NT - 1) / (4 * NT);
 };
 
 // x (and gain) float4s of the passes that hold blocks; lanes past the end read the last whole
 // float4 (the values are masked later). A row length that is not a multiple of 4 takes scalar loads.
-template <bool NORM>
+template <bool NORM, int NT>
 __device__ __forceinline__ void act_load(const qmh_mv_args &a, float4 *xr, float4 *wr) {
-    constexpr int P = ActRegs<NORM>::P;
+    constexpr int P = ActRegs<NORM, NT>::P;
     const int n = a.cols, tid = threadIdx.x;
     if ((n & 3) == 0) {
         const int q_last = (n >> 2) - 1;
         const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.norm_w;
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * QMH_WG * 4 < n) {
-                const int q = k * QMH_WG + tid, qc = q < q_last ? q : q_last;
+            if (k * NT * 4 < n) {
+                const int q = k * NT + tid, qc = q < q_last ? q : q_last;
                 xr[k] = x4[qc];
                 if (NORM) wr[k] = w4[qc];
             }
     } else {
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * QMH_WG * 4 < n) {
+            if (k * NT * 4 < n) {
                 float xv[4], wv[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const int i = 4 * (k * QMH_WG + tid) + j, ic = i < n ? i : n - 1;
+                    const int i = 4 * (k * NT + tid) + j, ic = i < n ? i : n - 1;
                     xv[j] = a.x[ic];
                     wv[j] = NORM ? a.norm_w[ic] : 0.0f;
                 }
@@ -121,21 +123,21 @@ struct ActDst {
     int ds, nrec;
 };
 
-template <bool SPLIT, bool NORM>
+template <bool SPLIT, bool NORM, int NT>
 __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 *wr, const ActDst &dst,
                            double *red) {
-    constexpr int P = ActRegs<NORM>::P;
+    constexpr int P = ActRegs<NORM, NT>::P;
     const int n = a.cols, nb = a.nb, tid = threadIdx.x, sub = tid & 7;
     float inv = 1.0f;
     if (NORM) {
         double ss = 0.0;
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * QMH_WG * 4 < n) {
+            if (k * NT * 4 < n) {
                 const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float xv = 4 * (k * QMH_WG + tid) + j < n ? xa[j] : 0.0f;
+                    const float xv = 4 * (k * NT + tid) + j < n ? xa[j] : 0.0f;
                     ss += (double)xv * (double)xv;
                 }
             }
@@ -154,8 +156,8 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
     }
 #pragma unroll
     for (int k = 0; k < P; k++) {
-        if (k * 32 >= nb) break;  // uniform
-        const int b = k * 32 + (tid >> 3), i4 = 4 * (k * QMH_WG + tid);
+        if (k * (NT / 8) >= nb) break;  // uniform
+        const int b = k * (NT / 8) + (tid >> 3), i4 = 4 * (k * NT + tid);
         const bool on = b < nb;
         const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
         float wa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -311,13 +313,22 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
 // activation modes of k_matvec: quantize x (optionally RMSNorm'd first), or copy a quantized
 // image another kernel wrote (QMH_XQ_IMAGE_BYTES layout)
 enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
-constexpr int MV_IMAGE_REGS = 4;  // uint4 per thread: images up to 16 KiB (nb <= 409)
+// uint4 per thread for an image of up to 16 KiB (nb <= 409)
+template <int NT>
+struct ImageRegs {
+    static constexpr int N = (16384 + 16 * NT - 1) / (16 * NT);
+};
 
 #ifndef QMH_MV_D
 #define QMH_MV_D 2  // chunks in flight per workgroup
 #endif
+// Timed on MI355X over the 7B shapes: 512 threads x 2 chunks x 2 Q4 slots (32 KiB of weights in
+// flight per workgroup) beat 256 threads x 4 slots by 6-20%, and every deeper or wider variant
 #ifndef QMH_MV_CH
-#define QMH_MV_CH 4  // Q4_0 slots per thread per chunk (Q8_0: half)
+#define QMH_MV_CH 2  // Q4_0 slots per thread per chunk (Q8_0: half)
+#endif
+#ifndef QMH_MV_NT
+#define QMH_MV_NT 512  // threads per workgroup
 #endif
 
 // ============================================================================ quantized matvec
@@ -348,24 +359,24 @@ constexpr int MV_REC = 48;  // LDS bytes per activation record
 __host__ __device__ __forceinline__ int mv_tile0(int w, int ntiles, int G) {
     return (int)((long long)w * ntiles / G);
 }
-__host__ __device__ __forceinline__ int mv_nrec(int nb, int R, int chq4, int dtype_q4) {
-    return nb + QMH_WG * (dtype_q4 ? chq4 : chq4 / 2) / R;
+__host__ __device__ __forceinline__ int mv_nrec(int nb, int R, int chq4, int dtype_q4, int nt) {
+    return nb + nt * (dtype_q4 ? chq4 : chq4 / 2) / R;
 }
 // dynamic LDS bytes of k_matvec: the records, then T for up to `tiles` tiles
-__host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, int tiles, int chq4, int dtype_q4) {
-    return (size_t)mv_nrec(nb, R, chq4, dtype_q4) * MV_REC + 4 * (size_t)tiles * R * nb;
+__host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, int tiles, int chq4, int dtype_q4, int nt) {
+    return (size_t)mv_nrec(nb, R, chq4, dtype_q4, nt) * MV_REC + 4 * (size_t)tiles * R * nb;
 }
 
 typedef unsigned int mv_u32x4 __attribute__((ext_vector_type(4)));
 
-template <int WT, int R, int AM, int D, int CHQ4>
-__global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
+template <int WT, int R, int AM, int D, int CHQ4, int NT>
+__global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     constexpr bool NORM = AM == MV_ACT_NORM;
     constexpr int CB = WT == QMH_Q4 ? 16 : 32;           // code bytes per block
     constexpr int NV = CB / 16;                          // uint4 per block
     constexpr int CH = WT == QMH_Q4 ? CHQ4 : CHQ4 / 2;   // slots per thread per chunk
-    constexpr int CHUNK = QMH_WG * CH;
-    static_assert(QMH_WG % R == 0 && CHUNK % R == 0, "a chunk holds whole block columns");
+    constexpr int CHUNK = NT * CH;
+    static_assert(NT % R == 0 && CHUNK % R == 0, "a chunk holds whole block columns");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
 
@@ -377,19 +388,19 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     float *T = (float *)(smem + (size_t)nrec * MV_REC);
 
     // 1. activation (or image) loads, issued first so waiting for them never waits for weights
-    float4 xr[AM == MV_ACT_IMAGE ? 1 : ActRegs<NORM>::P], wr[NORM ? ActRegs<NORM>::P : 1];
-    uint4 im[AM == MV_ACT_IMAGE ? MV_IMAGE_REGS : 1];
+    float4 xr[AM == MV_ACT_IMAGE ? 1 : ActRegs<NORM, NT>::P], wr[NORM ? ActRegs<NORM, NT>::P : 1];
+    uint4 im[AM == MV_ACT_IMAGE ? ImageRegs<NT>::N : 1];
     const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
     if (AM == MV_ACT_IMAGE) {
         const uint4 *src = (const uint4 *)a.xq_in;
 #pragma unroll
-        for (int k = 0; k < MV_IMAGE_REGS; k++)
-            if (k * QMH_WG < nimg) {
-                const int i = k * QMH_WG + tid;
+        for (int k = 0; k < ImageRegs<NT>::N; k++)
+            if (k * NT < nimg) {
+                const int i = k * NT + tid;
                 im[k] = src[i < nimg ? i : nimg - 1];
             }
     } else {
-        act_load<NORM>(a, xr, wr);
+        act_load<NORM, NT>(a, xr, wr);
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
 
@@ -402,7 +413,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     uint32_t Sc[D][CH];
 #define MV_LOAD(J, CHK)                                                                          \
     _Pragma("unroll") for (int k = 0; k < CH; k++) {                                              \
-        const int so = (CHK) * CHUNK + k * QMH_WG, left = nslot - so > 0 ? nslot - so : 0;        \
+        const int so = (CHK) * CHUNK + k * NT, left = nslot - so > 0 ? nslot - so : 0;        \
         const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(                      \
             (void *)(cbase + (size_t)so * CB), (short)0, left * CB, 0x00020000);                  \
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
@@ -426,9 +437,9 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     if (AM == MV_ACT_IMAGE) {
         // global image: codes [nb][32], then d [nb], then code sums [nb] (QMH_XQ_IMAGE_BYTES)
 #pragma unroll
-        for (int k = 0; k < MV_IMAGE_REGS; k++) {
-            const int i = k * QMH_WG + tid;
-            if (k * QMH_WG < nimg && i < nimg) {
+        for (int k = 0; k < ImageRegs<NT>::N; k++) {
+            const int i = k * NT + tid;
+            if (k * NT < nimg && i < nimg) {
                 const int o = 16 * i;
                 if (o < nb * 32) {
                     for (int rb = o / 32; rb < nrec; rb += nb)
@@ -448,7 +459,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
         }
         __syncthreads();
     } else {
-        act_finish<WT == QMH_Q4, NORM>(a, xr, wr,
+        act_finish<WT == QMH_Q4, NORM, NT>(a, xr, wr,
                                        ActDst{(int8_t *)smem, MV_REC, (float *)(smem + 32), (int *)(smem + 36),
                                               MV_REC / 4, nrec},
                                        red);
@@ -461,7 +472,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
     float *T_t = T + tid;
 #define MV_COMPUTE(J, CHK, UM, CHECK)                                                                   \
     _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
-        const uint8_t *rp = rec_t + ((UM) + k * (QMH_WG / R)) * MV_REC;                                 \
+        const uint8_t *rp = rec_t + ((UM) + k * (NT / R)) * MV_REC;                                 \
         const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);                                \
         const float2 ds = *(const float2 *)(rp + 32);                                                    \
         int acc;                                                                                         \
@@ -488,7 +499,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
             acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);                                   \
         }                                                                                                \
         const float t = (float)acc * (qmh_h2f((uint16_t)Sc[J][k]) * ds.x);                               \
-        if (!(CHECK) || (CHK) * CHUNK + k * QMH_WG + tid < nslot) T_t[(CHK) * CHUNK + k * QMH_WG] = t;  \
+        if (!(CHECK) || (CHK) * CHUNK + k * NT + tid < nslot) T_t[(CHK) * CHUNK + k * NT] = t;  \
     }
 
     int c0 = 0, um = 0;  // um: record of the chunk's first block column
@@ -515,7 +526,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec(qmh_mv_args a) {
 
     // 5. serial chains (row i of the range: tile i/R, row i%R; its terms at (tile*nb + b)*R + i%R)
     // and epilogues; a wave holds whole tiles (R divides 64, or R == 64)
-    for (int i0 = 0; i0 < rows_w; i0 += QMH_WG) {
+    for (int i0 = 0; i0 < rows_w; i0 += NT) {
         const int i = i0 + tid;
         if (i0 + (tid & ~63) >= rows_w) break;  // the whole wave is past the range
         const int tl = i / R, r = i % R, tile = t0 + tl;
@@ -577,14 +588,17 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
     mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e);
 }
 
-extern "C" int qmh_matvec_max_cols(int norm) { return (norm ? ActRegs<true>::P : ActRegs<false>::P) * QMH_WG * 4; }
+extern "C" int qmh_matvec_max_cols(int norm) {
+    return (norm ? ActRegs<true, QMH_MV_NT>::P : ActRegs<false, QMH_MV_NT>::P) * QMH_MV_NT * 4;
+}
 
 // Workgroups for k_matvec: `want` (about one per CU; more for matrices of many tiles), never
 // more than ntiles, and enough that a workgroup's records and terms fit the 64 KiB of LDS one
 // workgroup may take. -1: one tile does not fit.
 extern "C" int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int want) {
     if (ntiles < 1 || nb < 1 || (dtype != QMH_Q4 && dtype != QMH_Q8)) return -1;
-    const size_t rec = (size_t)mv_nrec(nb, tile_r, QMH_MV_CH, dtype == QMH_Q4) * MV_REC, per = 4 * (size_t)tile_r * nb;
+    const size_t rec = (size_t)mv_nrec(nb, tile_r, QMH_MV_CH, dtype == QMH_Q4, QMH_MV_NT) * MV_REC;
+    const size_t per = 4 * (size_t)tile_r * nb;
     if (rec + per > 65536) return -1;
     const int maxt = (int)((65536 - rec) / per);
     int g = want < ntiles ? want : ntiles;
@@ -598,14 +612,15 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
         return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     const int tmax = (a->ntiles + grid - 1) / grid;
-    const size_t lds = mv_lds_bytes(a->nb, a->tile_r, tmax, QMH_MV_CH, a->dtype == QMH_Q4);
+    const size_t lds = mv_lds_bytes(a->nb, a->tile_r, tmax, QMH_MV_CH, a->dtype == QMH_Q4, QMH_MV_NT);
     if (lds > 65536 || (long long)tmax * a->tile_r * a->nb * (a->dtype == QMH_Q4 ? 16 : 32) >= (1ll << 31))
         return (int)hipErrorInvalidValue;
-    if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)MV_IMAGE_REGS * QMH_WG * 16) return (int)hipErrorInvalidValue;
+    if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT>::N * QMH_MV_NT * 16) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_EPI_SWIGLU_Q) != (a->tile_r == 64)) return (int)hipErrorInvalidValue;
     const int am = image ? MV_ACT_IMAGE : norm ? MV_ACT_NORM : MV_ACT;
     hipStream_t s = (hipStream_t)stream;
-#define QMH_MV(WT, R, AM) hipLaunchKernelGGL((k_matvec<WT, R, AM, QMH_MV_D, QMH_MV_CH>), dim3(grid), dim3(QMH_WG), lds, s, *a)
+#define QMH_MV(WT, R, AM) \
+    hipLaunchKernelGGL((k_matvec<WT, R, AM, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a)
 #define QMH_MV_AM(WT, R)                                                  \
     if (am == MV_ACT_NORM) QMH_MV(WT, R, MV_ACT_NORM);                    \
     else if (am == MV_ACT_IMAGE) QMH_MV(WT, R, MV_ACT_IMAGE);             \

@@ -320,11 +320,11 @@ static void mv_args_for(const struct qmh_weight *w, qmh_mv_args *a) {
     a->rows = (int)w->rows;
 }
 
-/* one workgroup per CU; four per CU for matrices of many tiles (the output matrix), whose
+/* one workgroup per CU; two per CU for matrices of many tiles (the output matrix), whose
  * workgroups would otherwise each stream a long range behind a short prologue */
 static int mv_launch(const qmh_mv_args *a, hipStream_t s) {
     if (a->dtype == QMH_F32) return qmh_launch_matvec_f32(a, s);
-    const int want = g_cus * (a->ntiles >= 6 * g_cus ? 4 : 1);
+    const int want = g_cus * (a->ntiles >= 6 * g_cus ? 2 : 1);
     const int grid = qmh_matvec_grid(a->ntiles, a->nb, a->tile_r, a->dtype, want);
     return grid < 1 ? (int)hipErrorInvalidValue : qmh_launch_matvec(a, grid, s);
 }
