@@ -81,15 +81,19 @@ extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float
 
 // TC: positions per LDS chunk. 640 when the LDS holds it (group <= 8): a context of up to 640
 // positions is then one chunk, every V value of the workgroup requested at once.
-template <int TC>
+// MHA (one query head per kv head): the staged values are the products p_t*v_t, each rounded
+// as the reference rounds it, so the chain lanes only add.
+template <int TC, bool MHA>
 __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ att, const float *__restrict__ V,
                                                     float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
                                                     int n_kv, int hd, int max_seq) {
     constexpr int QMH_PV_TC = TC, QMH_PV_VS = TC + 4;  // V chunk row stride == 4 mod 64 floats
     static_assert(TC % 32 == 0 && TC * QMH_PV_CW % QMH_WG == 0, "whole 32-position steps, whole loads");
+    constexpr int SVK = 4;  // first head's scores kept in registers: positions < SVK*256
+    static_assert(!MHA || TC <= SVK * QMH_WG, "MHA probabilities of the first chunk come from registers");
     extern __shared__ __align__(16) float pv_smem[];
     float *P = pv_smem;                              // [group][TC] probabilities
-    float *Vs = pv_smem + (n_heads / n_kv) * TC;     // [CW][TC] the chunk, transposed
+    float *Vs = pv_smem + (n_heads / n_kv) * TC;     // [CW][TC] the chunk (V or, MHA, p*V), transposed
     __shared__ double red[16];
     __shared__ float redf[16];
     __shared__ float mx_s[16], inv_s[16];
@@ -101,6 +105,16 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
     constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
     float acc = 0.0f;
+    // the first head's scores (positions tid + 256k), issued first: the statistics wait for them only
+    float sv[SVK];
+    {
+        const float *s0 = att + (size_t)(kvh * group) * max_seq;
+#pragma unroll
+        for (int k = 0; k < SVK; k++) {
+            const int t = (int)threadIdx.x + k * QMH_WG;
+            sv[k] = s0[t < n ? t : 0];
+        }
+    }
     // a chunk's V values: unconditional, clamped loads, all in flight together (the first
     // chunk's under the softmax statistics); the next chunk's are issued before the current
     // chunk's chain runs
@@ -115,12 +129,24 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     // softmax statistics per head of the group (src/ops.c:100-112)
     for (int hl = 0; hl < group; hl++) {
         const float *s = att + (size_t)(kvh * group + hl) * max_seq;
+        float xv[SVK];
+#pragma unroll
+        for (int k = 0; k < SVK; k++) {
+            const int t = (int)threadIdx.x + k * QMH_WG;
+            xv[k] = hl == 0 ? sv[k] : s[t < n ? t : 0];
+        }
         float m = -__builtin_inff();
-        for (int t = threadIdx.x; t < n; t += QMH_WG) m = s[t] > m ? s[t] : m;
+#pragma unroll
+        for (int k = 0; k < SVK; k++)
+            if ((int)threadIdx.x + k * QMH_WG < n) m = xv[k] > m ? xv[k] : m;
+        for (int t = threadIdx.x + SVK * QMH_WG; t < n; t += QMH_WG) m = s[t] > m ? s[t] : m;
         m = qmh_block_max(m, redf);
         if (s[0] != s[0]) m = s[0];  // the reference's scan starts from x[0]: a NaN there stays
         double sum = 0.0;
-        for (int t = threadIdx.x; t < n; t += QMH_WG) sum += (double)qmh_expf(s[t] - m);
+#pragma unroll
+        for (int k = 0; k < SVK; k++)
+            if ((int)threadIdx.x + k * QMH_WG < n) sum += (double)qmh_expf(xv[k] - m);
+        for (int t = threadIdx.x + SVK * QMH_WG; t < n; t += QMH_WG) sum += (double)qmh_expf(s[t] - m);
         sum = qmh_block_sum_d(sum, red);
         const double d = qmh_sum_slack(sum, n);
         float inv = qmh_recip_of_sum(sum - d);
@@ -145,16 +171,26 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     for (int t0 = 0; t0 < n; t0 += QMH_PV_TC) {
         const int nt = min(QMH_PV_TC, n - t0);
         // probabilities of the chunk, +0 past nt
-        for (int e = threadIdx.x; e < group * QMH_PV_TC; e += QMH_WG) {
-            const int hl = e / QMH_PV_TC, t = e % QMH_PV_TC;
-            float p = 0.0f;
-            if (t < nt) p = qmh_expf(att[(size_t)(kvh * group + hl) * max_seq + t0 + t] - mx_s[hl]) * inv_s[hl];
-            P[hl * QMH_PV_TC + t] = p;
+        if (MHA && t0 == 0) {
+            const float m0 = mx_s[0], inv0 = inv_s[0];
+#pragma unroll
+            for (int k = 0; k < SVK; k++) {
+                const int t = (int)threadIdx.x + k * QMH_WG;
+                if (t < QMH_PV_TC) P[t] = t < nt ? qmh_expf(sv[k] - m0) * inv0 : 0.0f;
+            }
+        } else {
+            for (int e = threadIdx.x; e < group * QMH_PV_TC; e += QMH_WG) {
+                const int hl = e / QMH_PV_TC, t = e % QMH_PV_TC;
+                float p = 0.0f;
+                if (t < nt) p = qmh_expf(att[(size_t)(kvh * group + hl) * max_seq + t0 + t] - mx_s[hl]) * inv_s[hl];
+                P[hl * QMH_PV_TC + t] = p;
+            }
         }
+        if (MHA) __syncthreads();  // the products below read P
 #pragma unroll
         for (int k = 0; k < LPT; k++) {
             const int e = k * QMH_WG + threadIdx.x, t = e / QMH_PV_CW, cc = e % QMH_PV_CW;
-            Vs[cc * QMH_PV_VS + t] = t < nt ? vv[k] : 0.0f;
+            Vs[cc * QMH_PV_VS + t] = t < nt ? (MHA ? P[t] * vv[k] : vv[k]) : 0.0f;
         }
         if (t0 + QMH_PV_TC < n) QMH_PV_LOAD(t0 + QMH_PV_TC);
         __syncthreads();
@@ -168,7 +204,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
             float4 pc[8], vc[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                pc[j] = p4[j];
+                if (!MHA) pc[j] = p4[j];
                 vc[j] = v4[j];
             }
             for (int k = 0; k < n32; k++) {
@@ -176,19 +212,26 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
                 const int kn = k + 1 < n32 ? k + 1 : k;  // the last step re-reads itself
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    pn[j] = p4[8 * kn + j];
+                    if (!MHA) pn[j] = p4[8 * kn + j];
                     vn[j] = v4[8 * kn + j];
                 }
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    acc = acc + pc[j].x * vc[j].x;
-                    acc = acc + pc[j].y * vc[j].y;
-                    acc = acc + pc[j].z * vc[j].z;
-                    acc = acc + pc[j].w * vc[j].w;
+                    if (MHA) {  // the products were rounded when staged
+                        acc = acc + vc[j].x;
+                        acc = acc + vc[j].y;
+                        acc = acc + vc[j].z;
+                        acc = acc + vc[j].w;
+                    } else {
+                        acc = acc + pc[j].x * vc[j].x;
+                        acc = acc + pc[j].y * vc[j].y;
+                        acc = acc + pc[j].z * vc[j].z;
+                        acc = acc + pc[j].w * vc[j].w;
+                    }
                 }
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    pc[j] = pn[j];
+                    if (!MHA) pc[j] = pn[j];
                     vc[j] = vn[j];
                 }
             }
@@ -205,11 +248,12 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *
     if (group > 16 || group * QMH_PV_CW > QMH_WG) return (int)hipErrorInvalidValue;
     dim3 grid(n_kv_heads, (head_dim + QMH_PV_CW - 1) / QMH_PV_CW);
     hipStream_t s = (hipStream_t)stream;
-#define QMH_PV_GO(TC)                                                                                     \
-    hipLaunchKernelGGL(k_attn_pv<TC>, grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
+#define QMH_PV_GO(TC, MHA)                                                                                \
+    hipLaunchKernelGGL((k_attn_pv<TC, MHA>), grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
                        s, att, vcache, out, pos_ptr, n_heads, n_kv_heads, head_dim, max_seq)
-    if (group <= 8) QMH_PV_GO(640);
-    else QMH_PV_GO(256);
+    if (group == 1) QMH_PV_GO(640, true);
+    else if (group <= 8) QMH_PV_GO(640, false);
+    else QMH_PV_GO(256, false);
 #undef QMH_PV_GO
     return (int)hipGetLastError();
 }
