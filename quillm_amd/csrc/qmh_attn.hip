@@ -84,9 +84,9 @@ extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float
 // MHA (one query head per kv head): the staged values are the products p_t*v_t, each rounded
 // as the reference rounds it, so the chain lanes only add.
 template <int TC, bool MHA>
-__global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ att, const float *__restrict__ V,
-                                                    float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
-                                                    int n_kv, int hd, int max_seq) {
+__device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, const float *__restrict__ V,
+                                               float *__restrict__ out, const int n, int n_heads, int n_kv, int hd,
+                                               int max_seq) {
     constexpr int QMH_PV_TC = TC, QMH_PV_VS = TC + 4;  // V chunk row stride == 4 mod 64 floats
     static_assert(TC % 32 == 0 && TC * QMH_PV_CW % QMH_WG == 0, "whole 32-position steps, whole loads");
     constexpr int SVK = 4;  // first head's scores kept in registers: positions < SVK*256
@@ -97,8 +97,6 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     __shared__ double red[16];
     __shared__ float redf[16];
     __shared__ float mx_s[16], inv_s[16];
-    const int n = *pos_ptr + 1;
-    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
     const int kvh = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, group = n_heads / n_kv, kvd = hd * n_kv;
     const int lane_h = threadIdx.x / QMH_PV_CW, col = threadIdx.x % QMH_PV_CW;
     const bool chain = lane_h < group;
@@ -242,6 +240,152 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
 #undef QMH_PV_LOAD
 }
 
+template <int TC, bool MHA>
+__global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ att, const float *__restrict__ V,
+                                                    float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
+                                                    int n_kv, int hd, int max_seq) {
+    const int n = *pos_ptr + 1;
+    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
+    attn_pv_chunks<TC, MHA>(att, V, out, n, n_heads, n_kv, hd, max_seq);
+}
+
+// One query head per kv head, head_dim a multiple of 4, and (tested on the device) a context of
+// at most TC positions; longer contexts take attn_pv_chunks. Same sums in the same order, laid
+// out for a shorter critical path:
+//   * V is read as float4 (4 columns of one position per thread);
+//   * the softmax exponentials e_t stay in LDS (P) from the statistics to the products, and the
+//     serial fallback of the sum reads them there;
+//   * each reduction takes one barrier (its own LDS buffer);
+//   * the products p_t*v_t are staged in pieces of 128 positions: while the chain lanes (the
+//     first 16 threads, one output column each) add piece j, the other waves stage piece j+1.
+template <int TC>
+__global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict__ att, const float *__restrict__ V,
+                                                        float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
+                                                        int hd, int max_seq) {
+    constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
+    constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
+    constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
+    constexpr int PC = 128;                          // positions per staged piece
+    static_assert(QMH_PV_CW == 16 && TC % PC == 0 && (TC * QMH_PV_CW / 4) % QMH_WG == 0, "whole pieces, whole loads");
+    static_assert(PC * QMH_PV_CW / 4 == 2 * QMH_WG, "a piece is two float4 loads of every thread");
+    extern __shared__ __align__(16) float pv_smem[];
+    float *P = pv_smem;       // [TC] exponentials e_t
+    float *Vs = pv_smem + TC; // [CW][VS] products, transposed
+    __shared__ float wmax[QMH_WG / 64];
+    __shared__ double wsum[QMH_WG / 64];
+    __shared__ double ser_s;
+    const int n = *pos_ptr + 1;
+    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
+    if (n > TC) {
+        attn_pv_chunks<TC, true>(att, V, out, n, n_heads, n_heads, hd, max_seq);
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int h = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_heads;
+    const float *s0 = att + (size_t)h * max_seq;
+    // loads: the head's scores, then the V float4s (position k*64 + tid/4, columns c .. c+3;
+    // columns past hd re-read the last whole float4 and are never stored)
+    float sv[SK];
+#pragma unroll
+    for (int k = 0; k < SK; k++) {
+        const int t = tid + k * QMH_WG;
+        sv[k] = s0[t < n ? t : 0];
+    }
+    const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
+    float4 vv[L4];
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
+        vv[k] = *(const float4 *)(V + (size_t)tcl * kvd + (size_t)h * hd + cc);
+    }
+    // softmax statistics (src/ops.c:100-112): max (NaN never wins; a NaN at x[0] stays),
+    // e_t = expf(x_t - max) kept in P, the double sum as a tree checked against the serial order
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < SK; k++)
+        if (tid + k * QMH_WG < n) m = sv[k] > m ? sv[k] : m;
+    m = qmh_wave_max(m);
+    if (lane == 0) wmax[wv] = m;
+    __syncthreads();
+    m = wmax[0];
+#pragma unroll
+    for (int w = 1; w < QMH_WG / 64; w++) m = fmaxf(m, wmax[w]);
+    if (s0[0] != s0[0]) m = s0[0];
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < SK; k++) {
+        const int t = tid + k * QMH_WG;
+        if (t < n) {
+            const float e = qmh_expf(sv[k] - m);
+            P[t] = e;
+            sum += (double)e;
+        }
+    }
+    sum = qmh_wave_sum_d(sum);
+    if (lane == 0) wsum[wv] = sum;
+    __syncthreads();  // also publishes P
+    sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < QMH_WG / 64; w++) sum += wsum[w];
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform: the reference's serial order
+        if (tid == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)P[t];
+            ser_s = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(ser_s);
+    }
+    // products of piece j: this thread's float4s 2j and 2j+1; +0 past n (the chain's sum started
+    // at +0 and is never -0, so the padding changes nothing)
+    auto stage = [&](int j) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int k = 2 * j + u, t = k * (QMH_WG / 4) + (tid >> 2);
+            const bool on = t < n;
+            const float p = on ? P[t] * inv : 0.0f;
+            const float4 v = vv[k];
+            float *dst = Vs + (size_t)(4 * (tid & 3)) * VS + t;
+            dst[0] = on ? p * v.x : 0.0f;
+            dst[VS] = on ? p * v.y : 0.0f;
+            dst[2 * VS] = on ? p * v.z : 0.0f;
+            dst[3 * VS] = on ? p * v.w : 0.0f;
+        }
+    };
+    const int npc = (n + PC - 1) / PC;
+    const bool chain = tid < QMH_PV_CW;
+    const float4 *v4 = (const float4 *)(Vs + (size_t)(chain ? tid : 0) * VS);
+    float acc = 0.0f;
+    stage(0);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TC / PC; j++) {
+        if (j < npc) {  // uniform
+            if (j + 1 < npc) stage(j + 1);
+            if (chain) {
+                // out = out + p_t*v_t in t order, 32 positions per step
+#pragma unroll
+                for (int st = 0; st < PC / 32; st++) {
+                    float4 vc[8];
+#pragma unroll
+                    for (int q = 0; q < 8; q++) vc[q] = v4[j * (PC / 4) + st * 8 + q];
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        acc = acc + vc[q].x;
+                        acc = acc + vc[q].y;
+                        acc = acc + vc[q].z;
+                        acc = acc + vc[q].w;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (chain && i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
+}
+
 extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *out, const int32_t *pos_ptr,
                                   int n_heads, int n_kv_heads, int head_dim, int max_seq, void *stream) {
     const int group = n_heads / n_kv_heads;
@@ -251,7 +395,11 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *
 #define QMH_PV_GO(TC, MHA)                                                                                \
     hipLaunchKernelGGL((k_attn_pv<TC, MHA>), grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
                        s, att, vcache, out, pos_ptr, n_heads, n_kv_heads, head_dim, max_seq)
-    if (group == 1) QMH_PV_GO(640, true);
+    if (group == 1 && head_dim % 4 == 0)
+        hipLaunchKernelGGL(k_attn_pv_mha<640>, grid, dim3(QMH_WG),
+                           sizeof(float) * ((size_t)640 + QMH_PV_CW * (640 + 4)), s, att, vcache, out, pos_ptr, n_heads,
+                           head_dim, max_seq);
+    else if (group == 1) QMH_PV_GO(640, true);
     else if (group <= 8) QMH_PV_GO(640, false);
     else QMH_PV_GO(256, false);
 #undef QMH_PV_GO
