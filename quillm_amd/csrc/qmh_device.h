@@ -236,6 +236,17 @@ __device__ __forceinline__ float qmh_amax8(float m) {
     p = __int_as_float(qmh_dpp<QMH_DPP_HALF_MIRROR>(__float_as_int(m)));
     return p > m ? p : m;
 }
+// the same over the 4 lanes of a quad (lane ^ 1, then lane ^ 2)
+__device__ __forceinline__ float qmh_amax4(float m) {
+    float p = __int_as_float(qmh_dpp<QMH_DPP_QXOR1>(__float_as_int(m)));
+    m = p > m ? p : m;
+    p = __int_as_float(qmh_dpp<QMH_DPP_QXOR2>(__float_as_int(m)));
+    return p > m ? p : m;
+}
+__device__ __forceinline__ int qmh_sum4(int v) {
+    v += qmh_dpp<QMH_DPP_QXOR1>(v);
+    return v + qmh_dpp<QMH_DPP_QXOR2>(v);
+}
 __device__ __forceinline__ int qmh_sum8(int v) {
     v += qmh_dpp<QMH_DPP_QXOR1>(v);
     v += qmh_dpp<QMH_DPP_QXOR2>(v);

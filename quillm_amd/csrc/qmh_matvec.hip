@@ -63,25 +63,26 @@ extern "C" int qmh_launch_repack(const uint8_t *src, int64_t src_rows, int nb, i
 // is computed). With RMSNorm (NORM) the gain is applied first (src/ops.c:93-98), so the
 // normalised vector never round-trips through memory.
 //
-// Thread t holds float4 number k*256 + t of x (and of the gain) for every pass k: the loads are
-// coalesced, issued BEFORE the weight loads (the vector-memory counter retires loads in order,
-// so the prologue never waits for weights), and each thread's float4 is exactly the quarter
-// block it quantizes: block k*32 + t/8, elements 4*(t%8) .. +3. The 8 lanes of a block reduce
-// their amax and code sum with DPP. Results in LDS:
-//   acodes[b*32 + k]: the block's 32 codes. For Q4_0 weights they are stored split, even
-//                     elements in [0,16) and odd elements in [16,32), to match the weight's
-//                     low/high nibbles; asum[b] = sum of the codes.
-//   ad[b]            : fp32(fp16(d)) of the block.
+// Thread t holds 8 consecutive elements (two float4) of x (and of the gain) for every pass k:
+// elements 8*(k*NT + t) .. +7, i.e. a quarter of block k*NT/4 + t/4. The loads are coalesced and
+// issued BEFORE the weight loads (the vector-memory counter retires loads in order, so the
+// prologue never waits for weights); the 4 lanes of a block reduce its amax and code sum with
+// two DPP steps. Results in LDS, one 48-byte record per block:
+//   codes[b*48 + k]: the block's 32 codes. For Q4_0 weights they are stored split, even
+//                    elements in [0,16) and odd elements in [16,32), to match the weight's
+//                    low/high nibbles;
+//   d[b*12]        : fp32(fp16(d)) of the block;  sum[b*12]: the sum of its codes.
 
-// float4 of the activation per thread (passes) for NT threads: cols <= P*4*NT, at least 6144
-// with RMSNorm and 12288 without
+// float4 pairs of the activation per thread (passes) for NT threads: cols <= P*8*NT, at least
+// 6144 with RMSNorm and 12288 without
 template <bool NORM, int NT>
 struct ActRegs {
-    static constexpr int P = ((NORM ? 6144 : 12288) + 4 * NT - 1) / (4 * NT);
+    static constexpr int P = ((NORM ? 6144 : 12288) + 8 * NT - 1) / (8 * NT);
 };
 
-// x (and gain) float4s of the passes that hold blocks; lanes past the end read the last whole
-// float4 (the values are masked later). A row length that is not a multiple of 4 takes scalar loads.
+// x (and gain) float4 pairs of the passes that hold blocks; lanes past the end read the last
+// whole float4 (the values are masked later). A row length that is not a multiple of 4 takes
+// scalar loads.
 template <bool NORM, int NT>
 __device__ __forceinline__ void act_load(const qmh_mv_args &a, float4 *xr, float4 *wr) {
     constexpr int P = ActRegs<NORM, NT>::P;
@@ -91,24 +92,30 @@ __device__ __forceinline__ void act_load(const qmh_mv_args &a, float4 *xr, float
         const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.norm_w;
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * NT * 4 < n) {
-                const int q = k * NT + tid, qc = q < q_last ? q : q_last;
-                xr[k] = x4[qc];
-                if (NORM) wr[k] = w4[qc];
+            if (k * NT * 8 < n) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int q = 2 * (k * NT + tid) + h, qc = q < q_last ? q : q_last;
+                    xr[2 * k + h] = x4[qc];
+                    if (NORM) wr[2 * k + h] = w4[qc];
+                }
             }
     } else {
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * NT * 4 < n) {
-                float xv[4], wv[4];
+            if (k * NT * 8 < n) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int i = 4 * (k * NT + tid) + j, ic = i < n ? i : n - 1;
-                    xv[j] = a.x[ic];
-                    wv[j] = NORM ? a.norm_w[ic] : 0.0f;
+                for (int h = 0; h < 2; h++) {
+                    float xv[4], wv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int i = 8 * (k * NT + tid) + 4 * h + j, ic = i < n ? i : n - 1;
+                        xv[j] = a.x[ic];
+                        wv[j] = NORM ? a.norm_w[ic] : 0.0f;
+                    }
+                    xr[2 * k + h] = make_float4(xv[0], xv[1], xv[2], xv[3]);
+                    if (NORM) wr[2 * k + h] = make_float4(wv[0], wv[1], wv[2], wv[3]);
                 }
-                xr[k] = make_float4(xv[0], xv[1], xv[2], xv[3]);
-                if (NORM) wr[k] = make_float4(wv[0], wv[1], wv[2], wv[3]);
             }
     }
 }
@@ -127,70 +134,91 @@ template <bool SPLIT, bool NORM, int NT>
 __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 *wr, const ActDst &dst,
                            double *red) {
     constexpr int P = ActRegs<NORM, NT>::P;
-    const int n = a.cols, nb = a.nb, tid = threadIdx.x, sub = tid & 7;
+    const int n = a.cols, nb = a.nb, tid = threadIdx.x, sub = tid & 3;
     float inv = 1.0f;
     if (NORM) {
         double ss = 0.0;
 #pragma unroll
         for (int k = 0; k < P; k++)
-            if (k * NT * 4 < n) {
-                const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+            if (k * NT * 8 < n) {
+                const float xa[8] = {xr[2 * k].x,     xr[2 * k].y,     xr[2 * k].z,     xr[2 * k].w,
+                                     xr[2 * k + 1].x, xr[2 * k + 1].y, xr[2 * k + 1].z, xr[2 * k + 1].w};
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float xv = 4 * (k * NT + tid) + j < n ? xa[j] : 0.0f;
+                for (int j = 0; j < 8; j++) {
+                    const float xv = 8 * (k * NT + tid) + j < n ? xa[j] : 0.0f;
                     ss += (double)xv * (double)xv;
                 }
             }
-        ss = qmh_block_sum_d(ss, red);
+        // workgroup sum: wave butterflies, then the waves in order (red is not reused, so one
+        // barrier publishes the partials)
+        ss = qmh_wave_sum_d(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = 0.0;
+#pragma unroll
+        for (int w = 0; w < NT / 64; w++) ss += red[w];
         const double d = qmh_sum_slack(ss, nb * 32);
         inv = qmh_rms_inv(ss - d, n, a.eps);
         if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // same ss in every thread: uniform branch
             if (tid == 0) {
                 double s = 0.0;
                 for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
-                red[8] = s;  // red[0..3] hold the tree's partials; 8 is free
+                red[15] = s;  // red[0 .. NT/64) hold the partials; 15 is free
             }
             __syncthreads();
-            inv = qmh_rms_inv(red[8], n, a.eps);
+            inv = qmh_rms_inv(red[15], n, a.eps);
         }
     }
 #pragma unroll
     for (int k = 0; k < P; k++) {
-        if (k * (NT / 8) >= nb) break;  // uniform
-        const int b = k * (NT / 8) + (tid >> 3), i4 = 4 * (k * NT + tid);
+        if (k * (NT / 4) >= nb) break;  // uniform
+        const int b = k * (NT / 4) + (tid >> 2), i8 = 8 * (k * NT + tid);
         const bool on = b < nb;
-        const float xa[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
-        float wa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float xa[8] = {xr[2 * k].x,     xr[2 * k].y,     xr[2 * k].z,     xr[2 * k].w,
+                             xr[2 * k + 1].x, xr[2 * k + 1].y, xr[2 * k + 1].z, xr[2 * k + 1].w};
+        float wa[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         if (NORM) {
-            wa[0] = wr[k].x;
-            wa[1] = wr[k].y;
-            wa[2] = wr[k].z;
-            wa[3] = wr[k].w;
+            wa[0] = wr[2 * k].x;
+            wa[1] = wr[2 * k].y;
+            wa[2] = wr[2 * k].z;
+            wa[3] = wr[2 * k].w;
+            wa[4] = wr[2 * k + 1].x;
+            wa[5] = wr[2 * k + 1].y;
+            wa[6] = wr[2 * k + 1].z;
+            wa[7] = wr[2 * k + 1].w;
         }
-        float v[4], m = 0.0f;
+        float v[8], m = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float xv = (on && i4 + j < n) ? xa[j] : 0.0f;
+        for (int j = 0; j < 8; j++) {
+            float xv = (on && i8 + j < n) ? xa[j] : 0.0f;
             if (NORM) xv = xv * inv * wa[j];  // (x*inv)*w as the reference; 0 stays 0 past n
             v[j] = xv;
             const float av = fabsf(xv);
             m = av > m ? av : m;
         }
-        m = qmh_amax8(m);
+        m = qmh_amax4(m);
         const uint16_t dh = qmh_f2h(qmh_div127(m));
-        const float dd = qmh_h2f(dh);
-        int q[4];
-        qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
-        const int ps = qmh_sum8(q[0] + q[1] + q[2] + q[3]);
+        const float dd = qmh_h2f(dh), rinv = qmh_rcp(dd);
+        int q[8];
+        qmh_q8_codes4(v, dd, rinv, q);
+        qmh_q8_codes4(v + 4, dd, rinv, q + 4);
+        const int ps = qmh_sum4(q[0] + q[1] + q[2] + q[3] + q[4] + q[5] + q[6] + q[7]);
         if (on) {
+            uint2 w;  // the lane's 8 codes: SPLIT, evens then odds; else in order
+            if (SPLIT) {
+                w.x = (uint32_t)((q[0] & 0xff) | ((q[2] & 0xff) << 8) | ((q[4] & 0xff) << 16) | ((uint32_t)(q[6] & 0xff) << 24));
+                w.y = (uint32_t)((q[1] & 0xff) | ((q[3] & 0xff) << 8) | ((q[5] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24));
+            } else {
+                w.x = (uint32_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));
+                w.y = (uint32_t)((q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24));
+            }
             for (int rb = b; rb < dst.nrec; rb += nb) {
                 int8_t *c = dst.codes + rb * dst.cs;
                 if (SPLIT) {
-                    *(uint16_t *)(c + sub * 2) = (uint16_t)((q[0] & 0xff) | ((q[2] & 0xff) << 8));
-                    *(uint16_t *)(c + 16 + sub * 2) = (uint16_t)((q[1] & 0xff) | ((q[3] & 0xff) << 8));
+                    *(uint32_t *)(c + sub * 4) = w.x;
+                    *(uint32_t *)(c + 16 + sub * 4) = w.y;
                 } else {
-                    *(uint32_t *)(c + sub * 4) = (uint32_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8) |
-                                                            ((q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24));
+                    *(uint2 *)(c + sub * 8) = w;
                 }
                 if (sub == 0) {
                     dst.d[rb * dst.ds] = dd;
@@ -204,7 +232,7 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
                     o[1] = (uint8_t)(dh >> 8);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; j++) o[2 + sub * 4 + j] = (uint8_t)(int8_t)q[j];
+                for (int j = 0; j < 8; j++) o[2 + sub * 8 + j] = (uint8_t)(int8_t)q[j];
             }
         }
     }
@@ -349,7 +377,8 @@ struct ImageRegs {
 //     zeroes slots past the range without a memory access;
 //   * the activation in LDS as 48-byte records (32 codes, d, code sum), laid out unrolled:
 //     record j holds block j mod nb for j < nb + CHUNK/R, so a chunk's records are a scalar
-//     base plus a per-lane constant and nothing wraps;
+//     base plus a per-lane constant and nothing wraps (no vector work between a chunk's
+//     arrival and the next chunk's loads);
 //   * the terms in LDS in slot order (T[l] for the range's slot l), so the store address is a
 //     per-lane constant plus the chunk's base. After the last chunk every row's serial chain
 //     walks its terms (stride R), then the epilogue.
@@ -388,7 +417,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     float *T = (float *)(smem + (size_t)nrec * MV_REC);
 
     // 1. activation (or image) loads, issued first so waiting for them never waits for weights
-    float4 xr[AM == MV_ACT_IMAGE ? 1 : ActRegs<NORM, NT>::P], wr[NORM ? ActRegs<NORM, NT>::P : 1];
+    float4 xr[AM == MV_ACT_IMAGE ? 1 : 2 * ActRegs<NORM, NT>::P], wr[NORM ? 2 * ActRegs<NORM, NT>::P : 1];
     uint4 im[AM == MV_ACT_IMAGE ? ImageRegs<NT>::N : 1];
     const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
     if (AM == MV_ACT_IMAGE) {
@@ -465,14 +494,14 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
                                        red);
     }
 
-    // 4. the stream. Thread tid's slot k of chunk c is l = c*CHUNK + k*256 + tid: block
-    // column (l / R) = c*CHUNK/R + k*256/R + tid/R, record (that mod nb) = um + k*256/R + tid/R
-    // with um = (c*CHUNK/R) mod nb.
+    // 4. the stream. Thread tid's slot k of chunk c is l = c*CHUNK + k*NT + tid: block column
+    // (l / R) = c*CHUNK/R + k*NT/R + tid/R, record (that mod nb) = um + k*NT/R + tid/R in the
+    // unrolled layout, with um = (c*CHUNK/R) mod nb.
     const uint8_t *rec_t = smem + (tid / R) * MV_REC;
     float *T_t = T + tid;
 #define MV_COMPUTE(J, CHK, UM, CHECK)                                                                   \
     _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
-        const uint8_t *rp = rec_t + ((UM) + k * (NT / R)) * MV_REC;                                 \
+        const uint8_t *rp = rec_t + ((UM) + k * (NT / R)) * MV_REC;                                      \
         const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);                                \
         const float2 ds = *(const float2 *)(rp + 32);                                                    \
         int acc;                                                                                         \
@@ -589,7 +618,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
 }
 
 extern "C" int qmh_matvec_max_cols(int norm) {
-    return (norm ? ActRegs<true, QMH_MV_NT>::P : ActRegs<false, QMH_MV_NT>::P) * QMH_MV_NT * 4;
+    return (norm ? ActRegs<true, QMH_MV_NT>::P : ActRegs<false, QMH_MV_NT>::P) * QMH_MV_NT * 8;
 }
 
 // Workgroups for k_matvec: `want` (about one per CU; more for matrices of many tiles), never
