@@ -274,6 +274,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     __shared__ float wmax[QMH_WG / 64];
     __shared__ double wsum[QMH_WG / 64];
     __shared__ double ser_s;
+    __shared__ uint64_t etab[32];
     const int n = *pos_ptr + 1;
     if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
     if (n > TC) {
@@ -291,6 +292,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
         const int t = tid + k * QMH_WG;
         sv[k] = s0[t < n ? t : 0];
     }
+    qmh_exp_tab_fill(etab);  // published by the max's barrier
     const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
     float4 vv[L4];
 #pragma unroll
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     for (int k = 0; k < SK; k++) {
         const int t = tid + k * QMH_WG;
         if (t < n) {
-            const float e = qmh_expf(sv[k] - m);
+            const float e = qmh_expf_t(sv[k] - m, etab);
             P[t] = e;
             sum += (double)e;
         }
@@ -365,19 +367,17 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
         if (j < npc) {  // uniform
             if (j + 1 < npc) stage(j + 1);
             if (chain) {
-                // out = out + p_t*v_t in t order, 32 positions per step
+                // out = out + p_t*v_t in t order; the piece's terms are read at once, so the LDS
+                // latency is paid once per piece
+                float4 vc[PC / 4];
 #pragma unroll
-                for (int st = 0; st < PC / 32; st++) {
-                    float4 vc[8];
+                for (int q = 0; q < PC / 4; q++) vc[q] = v4[j * (PC / 4) + q];
 #pragma unroll
-                    for (int q = 0; q < 8; q++) vc[q] = v4[j * (PC / 4) + st * 8 + q];
-#pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        acc = acc + vc[q].x;
-                        acc = acc + vc[q].y;
-                        acc = acc + vc[q].z;
-                        acc = acc + vc[q].w;
-                    }
+                for (int q = 0; q < PC / 4; q++) {
+                    acc = acc + vc[q].x;
+                    acc = acc + vc[q].y;
+                    acc = acc + vc[q].z;
+                    acc = acc + vc[q].w;
                 }
             }
             __syncthreads();

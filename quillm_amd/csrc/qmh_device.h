@@ -61,7 +61,9 @@ __constant__ static const uint64_t qmh_exp2_tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float qmh_expf(float x) {
+// tab: the 32 entries of qmh_exp2_tab, wherever they are (a workgroup may keep a copy in LDS,
+// filled by qmh_exp_tab_fill before a barrier, to take the table lookup off global memory)
+__device__ __forceinline__ float qmh_expf_t(float x, const uint64_t *tab) {
     uint32_t ux = __float_as_uint(x);
     uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
@@ -79,7 +81,7 @@ __device__ __forceinline__ float qmh_expf(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = qmh_exp2_tab[ki % 32] + (ki << 47);
+    uint64_t t = tab[ki % 32] + (ki << 47);
     double s = __longlong_as_double((long long)t);
     double z = __builtin_fma(c0, r, c1);
     double r2 = r * r;
@@ -87,6 +89,11 @@ __device__ __forceinline__ float qmh_expf(float x) {
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+__device__ __forceinline__ float qmh_expf(float x) { return qmh_expf_t(x, qmh_exp2_tab); }
+// threads 0..31 copy the table to dst (LDS); visible to the workgroup after the next barrier
+__device__ __forceinline__ void qmh_exp_tab_fill(uint64_t *dst) {
+    if (threadIdx.x < 32) dst[threadIdx.x] = qmh_exp2_tab[threadIdx.x];
 }
 
 // --------------------------------------------------------------------------- reductions

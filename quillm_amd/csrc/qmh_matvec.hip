@@ -262,22 +262,22 @@ __device__ __forceinline__ EpiIn epi_fetch(const qmh_mv_args &a, int row, int po
     return e;
 }
 
-// Max and sum over the 64 lanes of a wave (all lanes end with the result): DPP inside groups
-// of 8, then lane ^ 8, ^ 16, ^ 32. NaN never wins the max.
-__device__ __forceinline__ float mv_wave_amax(float m) {
+// Max and sum over lanes 0..31 of a wave, every lane ending with the result: DPP inside groups
+// of 8, then lane ^ 8 (row rotate by 8), then lanes 0 and 16 read as scalars. The max takes
+// non-negative values with no NaN.
+#define MV_DPP_ROW_ROR8 0x128
+__device__ __forceinline__ float mv_amax32(float m) {
     m = qmh_amax8(m);
-#pragma unroll
-    for (int o = 8; o < 64; o <<= 1) {
-        const float p = __shfl_xor(m, o);
-        m = p > m ? p : m;
-    }
-    return m;
+    const float p = __int_as_float(qmh_dpp<MV_DPP_ROW_ROR8>(__float_as_int(m)));
+    m = p > m ? p : m;
+    const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    return m1 > m0 ? m1 : m0;
 }
-__device__ __forceinline__ int mv_wave_sum(int v) {
+__device__ __forceinline__ int mv_sum32(int v) {
     v = qmh_sum8(v);
-#pragma unroll
-    for (int o = 8; o < 64; o <<= 1) v += __shfl_xor(v, o);
-    return v;
+    v += qmh_dpp<MV_DPP_ROW_ROR8>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16);
 }
 
 // y: the row's result. Lanes of one tile hold consecutive rows, so the RoPE partner of row
@@ -285,7 +285,7 @@ __device__ __forceinline__ int mv_wave_sum(int v) {
 // K goes to a transposed cache [kvd][max_seq], V to a row cache [max_seq][kvd].
 template <int R>
 __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float y, int lane, int pos,
-                                            const EpiIn &e) {
+                                            const EpiIn &e, const uint64_t *etab) {
     switch (a.epi) {
     case QMH_EPI_STORE:
         if (row < a.rows) a.out0[row] = y;
@@ -309,20 +309,24 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
     }
     case QMH_EPI_SWIGLU: {  // silu(g)*u (src/ops.c:128-133)
         const float up = __shfl_down(y, R / 2);
-        if (lane < R / 2 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf(-y)) * up;
+        if (lane < R / 2 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf_t(-y, etab)) * up;
         break;
     }
     case QMH_EPI_SWIGLU_Q: {  // R == 64: lanes 0..31 hold the block (rows 32*b ..), 0 past rows
-        const float up = __shfl_down(y, R / 2);
+        // the W3 row of lane l (< 32) is lane l + 32: lanes 32..63 swapped into 0..31
+        const float up = __uint_as_float(
+            __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false)[1]);
         const bool mine = lane < R / 2 && row < a.rows;
-        const float h = mine ? y / (1.0f + qmh_expf(-y)) * up : 0.0f;
+        const float h = mine ? y / (1.0f + qmh_expf_t(-y, etab)) * up : 0.0f;
         if (mine && a.out0) a.out0[row] = h;
-        // the next matvec's activation block, as qm_quantize_row_q8 makes it (src/quant.c:55-63)
-        const float m = mv_wave_amax(fabsf(h));
+        // the next matvec's activation block, as qm_quantize_row_q8 makes it (src/quant.c:55-63):
+        // its amax starts at 0 and takes a value only when greater, so a NaN never counts
+        const float ah = fabsf(h);
+        const float m = mv_amax32(ah > 0.0f ? ah : 0.0f);
         const uint16_t dh = qmh_f2h(qmh_div127(m));
         const float dd = qmh_h2f(dh);
         const int q = qmh_q8_code_fast(h, dd, qmh_rcp(dd));
-        const int qs = mv_wave_sum(q);
+        const int qs = mv_sum32(q);
         if (lane < R / 2) {
             const int b = (row - lane) >> 5;
             uint8_t *img = (uint8_t *)a.xq_img;
@@ -408,6 +412,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     static_assert(NT % R == 0 && CHUNK % R == 0, "a chunk holds whole block columns");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
+    __shared__ uint64_t etab[32];  // expf's table for the SwiGLU epilogues
 
     const int nb = a.nb, TB = R * nb, tid = threadIdx.x;
     const int t0 = mv_tile0(blockIdx.x, a.ntiles, gridDim.x), t1 = mv_tile0(blockIdx.x + 1, a.ntiles, gridDim.x);
@@ -432,6 +437,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
         act_load<NORM, NT>(a, xr, wr);
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
+    if (a.epi == QMH_EPI_SWIGLU || a.epi == QMH_EPI_SWIGLU_Q) qmh_exp_tab_fill(etab);  // read after the barriers below
 
     // 2. the first D chunks. Each load's resource starts at its own 256 slots and holds what is
     // left of the range, so the range check (on the lane's offset) zeroes slots past the range
@@ -575,7 +581,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
             }
             for (; b < nb; b++) y = y + tp[b * R];
         }
-        mv_epilogue<R>(a, mine ? row : a.rows, y, r, pos, ein);
+        mv_epilogue<R>(a, mine ? row : a.rows, y, r, pos, ein, etab);
     }
 }
 
@@ -614,7 +620,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
     for (int i = 0; i < n; i++) s = s + w[i] * xs[i];
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
     const EpiIn e = epi_fetch(a, row, pos);
-    mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e);
+    mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e, qmh_exp2_tab);
 }
 
 extern "C" int qmh_matvec_max_cols(int norm) {
