@@ -56,6 +56,8 @@ SMALL_SHAPES = {
     "mha": dict(dim=96, hidden_dim=256, n_layers=2, n_heads=3, n_kv_heads=3, vocab_size=300, max_seq=48),
     # 12 query heads on one kv head, and a context past one 256-position attention chunk
     "gqa": dict(dim=96, hidden_dim=256, n_layers=2, n_heads=12, n_kv_heads=1, vocab_size=300, max_seq=300),
+    # 2 query heads per kv head of 48 dims: the K-tile scores kernel, over two 64-position tiles
+    "gqa48": dict(dim=192, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=136),
 }
 
 

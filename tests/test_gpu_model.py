@@ -20,13 +20,15 @@ def say(*a):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("shape", ["small", "odd", "mha", "gqa"])
+@pytest.mark.parametrize("shape", ["small", "odd", "mha", "gqa", "gqa48"])
 @pytest.mark.parametrize("wt", ["f32", "q8_0", "q4_0"])
 def test_forward_matches_oracle(gpu, oracle, small_models, shape, wt):
     path = small_models[(shape, wt)]
     say(f"case {shape}/{wt}: load {path}")
-    # gqa: 270 prompt tokens, so the attention context passes one 256-position chunk
-    prompt = gpu.prompt_ids(270 if shape == "gqa" else 6, 300 if shape in ("mha", "gqa") else 458, seed=5)
+    # gqa: 270 prompt tokens, so the attention context passes one 256-position chunk;
+    # gqa48: 100, so the scores cover two 64-position K tiles
+    n_prompt = {"gqa": 270, "gqa48": 100}.get(shape, 6)
+    prompt = gpu.prompt_ids(n_prompt, 458 if shape in ("small", "odd") else 300, seed=5)
     want, want_ids = oracle.run_model(path, prompt, n_gen=20)
     with gpu.Model.load(path) as m:
         got = []
