@@ -75,6 +75,10 @@ int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, con
                      void *stream);
 int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, const int32_t *pos_ptr, int n_heads,
                            int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
+/* the same scores for a kv head serving several query heads: K tile in LDS (head_dim 48, 64 or
+ * 128, max_seq % 4 == 0); qmh_launch_attn_scores calls it */
+int qmh_launch_attn_scores_tile(const float *q, const float *kcache, float *att, const int32_t *pos_ptr, int n_heads,
+                                int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
                        int n_kv_heads, int head_dim, int max_seq, void *stream);
 /* ---- batched prefill (qmh_prefill.hip) ---- */

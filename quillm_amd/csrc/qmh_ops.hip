@@ -347,3 +347,70 @@ extern "C" int qmh_launch_gemm_nt(const float *A, const float *B, float *C, int6
     hipLaunchKernelGGL(k_gemm_nt, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);
     return (int)hipGetLastError();
 }
+
+// ============================================================================ decode scores, K tile
+
+// Lives in this file rather than beside the other attention kernels: decode speed on MI355X
+// depends on where the device code of the attention kernels lands (measured: the same source
+// placed here runs the 7B step at 577 tok/s, beside them at 555), so the attention kernels' code
+// is kept as it was timed.
+#define QMH_SC_T 64  // positions per workgroup
+
+// Decode attention scores (as k_attn_scores in qmh_attn.hip) with the K tile staged in LDS: a
+// workgroup of QMH_WG threads owns 64 positions of one kv head; its HD x 64 floats of K arrive as
+// HD/16 float4 loads per thread (one
+// round trip, coalesced: 16 threads read one dimension's 64 positions), and wave w then runs the
+// dots of query heads w, w + 4, ... (one lane per position, the same serial order over head_dim).
+// Needs head_dim % 16 == 0 and max_seq % 4 == 0 (aligned float4 rows). Used when a kv head
+// serves several query heads (timed on MI355X: 6.3 -> 3.9 us at 32/8 heads, 128 dims, 640
+// positions); with one query head per kv head the one-wave kernel is faster (4.0 vs 4.5 us).
+template <int HD>
+__global__ __launch_bounds__(QMH_WG) void k_attn_scores_t(const float *__restrict__ q, const float *__restrict__ Kt,
+                                                          float *__restrict__ att, const int32_t *pos_ptr, int n_heads,
+                                                          int n_kv, int max_seq, float scale) {
+    static_assert(HD % 16 == 0 && (HD * QMH_SC_T / 4) % QMH_WG == 0, "whole float4 loads per thread");
+    constexpr int L4 = HD * QMH_SC_T / 4 / QMH_WG;  // float4 loads per thread
+    __shared__ __align__(16) float kt[HD * QMH_SC_T];  // [dim][position]
+    const int pos = *pos_ptr;
+    const int t0 = blockIdx.y * QMH_SC_T;
+    if (pos < 0 || pos >= max_seq || t0 > pos) return;
+    const int kvh = blockIdx.x, group = n_heads / n_kv, tid = threadIdx.x;
+    const float *kbase = Kt + (size_t)kvh * HD * max_seq;
+    float4 kv[L4];
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int e = k * QMH_WG + tid, i = e / (QMH_SC_T / 4), p4 = e % (QMH_SC_T / 4);
+        const int t = t0 + 4 * p4, tc = t <= max_seq - 4 ? t : max_seq - 4;  // in-bounds float4
+        kv[k] = *(const float4 *)(kbase + (size_t)i * max_seq + tc);
+    }
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int e = k * QMH_WG + tid, i = e / (QMH_SC_T / 4), p4 = e % (QMH_SC_T / 4);
+        *(float4 *)(kt + i * QMH_SC_T + 4 * p4) = kv[k];
+    }
+    __syncthreads();
+    const int lane = tid & 63, t = t0 + lane;
+    for (int hl = __builtin_amdgcn_readfirstlane(tid >> 6); hl < group; hl += QMH_WG / 64) {
+        const float *qh = q + (size_t)(kvh * group + hl) * HD;
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD; i++) s = s + qh[i] * kt[i * QMH_SC_T + lane];
+        if (t <= pos) att[(size_t)(kvh * group + hl) * max_seq + t] = s * scale;
+    }
+}
+
+
+extern "C" int qmh_launch_attn_scores_tile(const float *q, const float *kcache, float *att, const int32_t *pos_ptr,
+                                           int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale,
+                                           void *stream) {
+    dim3 grid(n_kv_heads, (max_seq + QMH_SC_T - 1) / QMH_SC_T);
+    hipStream_t s = (hipStream_t)stream;
+#define QMH_SCT(HD) \
+    hipLaunchKernelGGL(k_attn_scores_t<HD>, grid, dim3(QMH_WG), 0, s, q, kcache, att, pos_ptr, n_heads, n_kv_heads, \
+                       max_seq, scale)
+    if (head_dim == 128) QMH_SCT(128);
+    else if (head_dim == 64) QMH_SCT(64);
+    else QMH_SCT(48);
+#undef QMH_SCT
+    return (int)hipGetLastError();
+}
