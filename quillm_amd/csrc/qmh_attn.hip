@@ -345,21 +345,26 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
         __syncthreads();
         inv = qmh_recip_of_sum(ser_s);
     }
-    // products of piece j: this thread's float4s 2j and 2j+1; +0 past n (the chain's sum started
-    // at +0 and is never -0, so the padding changes nothing)
+    // products of piece j (positions j*PC ..): this thread's float4s 2j and 2j+1, which the loop
+    // below keeps in vv[0], vv[1] (the V registers rotate by two per piece, so one copy of the
+    // code serves every piece: the kernel's code stays small, and with it the instruction
+    // fetches of every launch); +0 past n (the chain's sum started at +0 and is never -0, so the
+    // padding changes nothing)
     auto stage = [&](int j) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-            const int k = 2 * j + u, t = k * (QMH_WG / 4) + (tid >> 2);
+            const int t = (2 * j + u) * (QMH_WG / 4) + (tid >> 2);
             const bool on = t < n;
             const float p = on ? P[t] * inv : 0.0f;
-            const float4 v = vv[k];
+            const float4 v = vv[u];
             float *dst = Vs + (size_t)(4 * (tid & 3)) * VS + t;
             dst[0] = on ? p * v.x : 0.0f;
             dst[VS] = on ? p * v.y : 0.0f;
             dst[2 * VS] = on ? p * v.z : 0.0f;
             dst[3 * VS] = on ? p * v.w : 0.0f;
         }
+#pragma unroll
+        for (int k = 0; k + 2 < L4; k++) vv[k] = vv[k + 2];
     };
     const int npc = (n + PC - 1) / PC;
     const bool chain = tid < QMH_PV_CW;
@@ -367,26 +372,24 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     float acc = 0.0f;
     stage(0);
     __syncthreads();
+#pragma nounroll
+    for (int j = 0; j < npc; j++) {  // uniform trip count
+        if (j + 1 < npc) stage(j + 1);
+        if (chain) {
+            // out = out + p_t*v_t in t order; the piece's terms are read at once, so the LDS
+            // latency is paid once per piece
+            float4 vc[PC / 4];
 #pragma unroll
-    for (int j = 0; j < TC / PC; j++) {
-        if (j < npc) {  // uniform
-            if (j + 1 < npc) stage(j + 1);
-            if (chain) {
-                // out = out + p_t*v_t in t order; the piece's terms are read at once, so the LDS
-                // latency is paid once per piece
-                float4 vc[PC / 4];
+            for (int q = 0; q < PC / 4; q++) vc[q] = v4[j * (PC / 4) + q];
 #pragma unroll
-                for (int q = 0; q < PC / 4; q++) vc[q] = v4[j * (PC / 4) + q];
-#pragma unroll
-                for (int q = 0; q < PC / 4; q++) {
-                    acc = acc + vc[q].x;
-                    acc = acc + vc[q].y;
-                    acc = acc + vc[q].z;
-                    acc = acc + vc[q].w;
-                }
+            for (int q = 0; q < PC / 4; q++) {
+                acc = acc + vc[q].x;
+                acc = acc + vc[q].y;
+                acc = acc + vc[q].z;
+                acc = acc + vc[q].w;
             }
-            __syncthreads();
         }
+        __syncthreads();
     }
     if (chain && i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
 }

@@ -157,6 +157,35 @@ __device__ __forceinline__ float qmh_rms_inv(double ss, int n, float eps) {
 }
 __device__ __forceinline__ float qmh_recip_of_sum(double s) { return (float)(1.0 / s); }
 
+// qmh_rms_inv for a sum known only to within the tree bound, without the correctly rounded
+// double chain when the answer is clear. s: a tree sum of nterms squares; n: the row length.
+// y = 1/sqrt(s/n + eps) from v_rsq_f64 (specified to 2^29 ulp, ~2^-23 relative) and two Newton
+// steps (error 1.5*e^2 plus rounding, below 2^-50). For the serial sum S, |S - s| <= d with
+// d/s = (nterms*2.5 + 8)*2^-53 (qmh_sum_slack), and the reference's double before its final
+// rounding, fl(1/fl(sqrt(fl(fl(S/n) + eps)))), is within a relative d/(2s) + 3*2^-53 of
+// 1/sqrt(S/n + eps), hence within M = y*(d/(2s) + 2^-46) of y. If y is farther than M from both
+// midpoints between fl32(y) and its float neighbours, the reference rounds to fl32(y) too (never
+// to a tie) and *out gets it; otherwise (relatively ~2^-16 of the inputs) it returns false and
+// the caller takes the exact path.
+__device__ __forceinline__ bool qmh_rms_inv_margin(double s, int n, int nterms, float eps, float *out) {
+    const double x = s * (1.0 / (double)n) + (double)eps;
+    double y = __builtin_amdgcn_rsq(x);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const double t = x * y;
+        const double e = __builtin_fma(-t, y, 1.0);
+        y = __builtin_fma(0.5 * y, e, y);
+    }
+    const float f = (float)y;
+    const uint32_t fb = __float_as_uint(f);
+    const double lo = 0.5 * ((double)f + (double)__uint_as_float(fb - 1u));
+    const double hi = 0.5 * ((double)f + (double)__uint_as_float(fb + 1u));
+    const double m = y * (((double)nterms * 2.5 + 8.0) * 0x1p-54 + 0x1p-46);
+    *out = f;
+    // finite, positive, normal: anything else (and every NaN comparison) goes the exact way
+    return s >= 0.0 && y < 0x1p100 && fb > 0x00800000u && fb < 0x7f000000u && y - m > lo && y + m < hi;
+}
+
 __device__ __forceinline__ float qmh_block_max(float v, float *buf) {
     v = qmh_wave_max(v);
     const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;

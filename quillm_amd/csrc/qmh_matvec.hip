@@ -157,16 +157,19 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
         ss = 0.0;
 #pragma unroll
         for (int w = 0; w < NT / 64; w++) ss += red[w];
-        const double d = qmh_sum_slack(ss, nb * 32);
-        inv = qmh_rms_inv(ss - d, n, a.eps);
-        if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // same ss in every thread: uniform branch
-            if (tid == 0) {
-                double s = 0.0;
-                for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
-                red[15] = s;  // red[0 .. NT/64) hold the partials; 15 is free
+        // same ss in every thread: uniform branches
+        if (!qmh_rms_inv_margin(ss, n, nb * 32, a.eps, &inv)) {
+            const double d = qmh_sum_slack(ss, nb * 32);
+            inv = qmh_rms_inv(ss - d, n, a.eps);
+            if (inv != qmh_rms_inv(ss + d, n, a.eps)) {
+                if (tid == 0) {
+                    double s = 0.0;
+                    for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
+                    red[15] = s;  // red[0 .. NT/64) hold the partials; 15 is free
+                }
+                __syncthreads();
+                inv = qmh_rms_inv(red[15], n, a.eps);
             }
-            __syncthreads();
-            inv = qmh_rms_inv(red[15], n, a.eps);
         }
     }
 #pragma unroll
@@ -283,8 +286,8 @@ __device__ __forceinline__ int mv_sum32(int v) {
 // y: the row's result. Lanes of one tile hold consecutive rows, so the RoPE partner of row
 // 2i/2i+1 is lane ^ 1 and the W3 partner of an interleaved W1 row is lane + R/2.
 // K goes to a transposed cache [kvd][max_seq], V to a row cache [max_seq][kvd].
-template <int R>
-__device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float y, int lane, int pos,
+// half: R/2 of the tile (the SwiGLU epilogues; 32 for SWIGLU_Q)
+__device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float y, int lane, int half, int pos,
                                             const EpiIn &e, const uint64_t *etab) {
     switch (a.epi) {
     case QMH_EPI_STORE:
@@ -308,15 +311,15 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
         break;
     }
     case QMH_EPI_SWIGLU: {  // silu(g)*u (src/ops.c:128-133)
-        const float up = __shfl_down(y, R / 2);
-        if (lane < R / 2 && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf_t(-y, etab)) * up;
+        const float up = __shfl_down(y, half);
+        if (lane < half && row < a.rows) a.out0[row] = y / (1.0f + qmh_expf_t(-y, etab)) * up;
         break;
     }
     case QMH_EPI_SWIGLU_Q: {  // R == 64: lanes 0..31 hold the block (rows 32*b ..), 0 past rows
         // the W3 row of lane l (< 32) is lane l + 32: lanes 32..63 swapped into 0..31
         const float up = __uint_as_float(
             __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false)[1]);
-        const bool mine = lane < R / 2 && row < a.rows;
+        const bool mine = lane < 32 && row < a.rows;
         const float h = mine ? y / (1.0f + qmh_expf_t(-y, etab)) * up : 0.0f;
         if (mine && a.out0) a.out0[row] = h;
         // the next matvec's activation block, as qm_quantize_row_q8 makes it (src/quant.c:55-63):
@@ -327,7 +330,7 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
         const float dd = qmh_h2f(dh);
         const int q = qmh_q8_code_fast(h, dd, qmh_rcp(dd));
         const int qs = mv_sum32(q);
-        if (lane < R / 2) {
+        if (lane < 32) {
             const int b = (row - lane) >> 5;
             uint8_t *img = (uint8_t *)a.xq_img;
             const int at = a.xq_split ? ((lane & 1) ? 16 + (lane >> 1) : (lane >> 1)) : lane;
@@ -402,30 +405,53 @@ __host__ __device__ __forceinline__ size_t mv_lds_bytes(int nb, int R, int tiles
 
 typedef unsigned int mv_u32x4 __attribute__((ext_vector_type(4)));
 
-template <int WT, int R, int AM, int D, int CHQ4, int NT>
+// one row's serial chain over its nb terms at stride R: y = +0; y = y + t_b in block order
+template <int R>
+__device__ __forceinline__ float mv_chain(const float *tp, int nb) {
+    float y = 0.0f;
+    int b = 0;
+    for (; b + 32 <= nb; b += 32) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 32; k++) v[k] = tp[(b + k) * R];
+#pragma unroll
+        for (int k = 0; k < 32; k++) y = y + v[k];
+    }
+    for (; b < nb; b++) y = y + tp[b * R];
+    return y;
+}
+
+// One instance per weight type serves every matvec of the token (tile height R and activation
+// mode are uniform runtime values): the decode step's kernels then share one copy of this code in
+// the instruction cache, instead of refetching a different instance's code (from HBM, the
+// weight stream having evicted it from L2) at every launch.
+template <int WT, int D, int CHQ4, int NT>
 __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
-    constexpr bool NORM = AM == MV_ACT_NORM;
     constexpr int CB = WT == QMH_Q4 ? 16 : 32;           // code bytes per block
     constexpr int NV = CB / 16;                          // uint4 per block
     constexpr int CH = WT == QMH_Q4 ? CHQ4 : CHQ4 / 2;   // slots per thread per chunk
     constexpr int CHUNK = NT * CH;
-    static_assert(NT % R == 0 && CHUNK % R == 0, "a chunk holds whole block columns");
+    constexpr int PX = ActRegs<false, NT>::P > ActRegs<true, NT>::P ? ActRegs<false, NT>::P : ActRegs<true, NT>::P;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
     __shared__ uint64_t etab[32];  // expf's table for the SwiGLU epilogues
 
+    // R (8, 16, 32 or 64: divides 64, so a chunk holds whole block columns) and the activation
+    // mode, both uniform
+    const int R = a.tile_r, lgR = __builtin_ctz((unsigned)R);
+    const int am = a.xq_in ? MV_ACT_IMAGE : a.norm_w ? MV_ACT_NORM : MV_ACT;
     const int nb = a.nb, TB = R * nb, tid = threadIdx.x;
     const int t0 = mv_tile0(blockIdx.x, a.ntiles, gridDim.x), t1 = mv_tile0(blockIdx.x + 1, a.ntiles, gridDim.x);
     const int ntw = t1 - t0, nslot = ntw * TB, nch = (nslot + CHUNK - 1) / CHUNK;
     if (ntw <= 0) return;  // the host launches at most ntiles workgroups
-    const int nrec = nb + CHUNK / R;
+    const int nrec = nb + (CHUNK >> lgR);
     float *T = (float *)(smem + (size_t)nrec * MV_REC);
 
     // 1. activation (or image) loads, issued first so waiting for them never waits for weights
-    float4 xr[AM == MV_ACT_IMAGE ? 1 : 2 * ActRegs<NORM, NT>::P], wr[NORM ? 2 * ActRegs<NORM, NT>::P : 1];
-    uint4 im[AM == MV_ACT_IMAGE ? ImageRegs<NT>::N : 1];
+    float4 xr[2 * PX], wr[2 * ActRegs<true, NT>::P];
+    uint4 im[ImageRegs<NT>::N];
     const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
-    if (AM == MV_ACT_IMAGE) {
+    if (am == MV_ACT_IMAGE) {
         const uint4 *src = (const uint4 *)a.xq_in;
 #pragma unroll
         for (int k = 0; k < ImageRegs<NT>::N; k++)
@@ -433,8 +459,10 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
                 const int i = k * NT + tid;
                 im[k] = src[i < nimg ? i : nimg - 1];
             }
+    } else if (am == MV_ACT_NORM) {
+        act_load<true, NT>(a, xr, wr);
     } else {
-        act_load<NORM, NT>(a, xr, wr);
+        act_load<false, NT>(a, xr, wr);
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
     if (a.epi == QMH_EPI_SWIGLU || a.epi == QMH_EPI_SWIGLU_Q) qmh_exp_tab_fill(etab);  // read after the barriers below
@@ -464,12 +492,12 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     const int rows_w = ntw * R;
     EpiIn ein = {0.0f, 1.0f, 0.0f};
     if (tid < rows_w) {
-        const int tile = t0 + tid / R, r = tid % R;
+        const int tile = t0 + (tid >> lgR), r = tid & (R - 1);
         ein = epi_fetch(a, R >= 2 * QMH_TILE_R ? tile * (R / 2) + (r & (R / 2 - 1)) : tile * R + r, pos);
     }
 
     // 3. the activation records
-    if (AM == MV_ACT_IMAGE) {
+    if (am == MV_ACT_IMAGE) {
         // global image: codes [nb][32], then d [nb], then code sums [nb] (QMH_XQ_IMAGE_BYTES)
 #pragma unroll
         for (int k = 0; k < ImageRegs<NT>::N; k++) {
@@ -494,20 +522,20 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
         }
         __syncthreads();
     } else {
-        act_finish<WT == QMH_Q4, NORM, NT>(a, xr, wr,
-                                       ActDst{(int8_t *)smem, MV_REC, (float *)(smem + 32), (int *)(smem + 36),
-                                              MV_REC / 4, nrec},
-                                       red);
+        const ActDst dst{(int8_t *)smem, MV_REC, (float *)(smem + 32), (int *)(smem + 36), MV_REC / 4, nrec};
+        if (am == MV_ACT_NORM) act_finish<WT == QMH_Q4, true, NT>(a, xr, wr, dst, red);
+        else act_finish<WT == QMH_Q4, false, NT>(a, xr, wr, dst, red);
     }
 
     // 4. the stream. Thread tid's slot k of chunk c is l = c*CHUNK + k*NT + tid: block column
     // (l / R) = c*CHUNK/R + k*NT/R + tid/R, record (that mod nb) = um + k*NT/R + tid/R in the
     // unrolled layout, with um = (c*CHUNK/R) mod nb.
-    const uint8_t *rec_t = smem + (tid / R) * MV_REC;
+    const uint8_t *rec_t = smem + (tid >> lgR) * MV_REC;
+    const int ntr = NT >> lgR;  // block columns per NT slots
     float *T_t = T + tid;
 #define MV_COMPUTE(J, CHK, UM, CHECK)                                                                   \
     _Pragma("unroll") for (int k = 0; k < CH; k++) {                                                     \
-        const uint8_t *rp = rec_t + ((UM) + k * (NT / R)) * MV_REC;                                      \
+        const uint8_t *rp = rec_t + ((UM) + k * ntr) * MV_REC;                                           \
         const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);                                \
         const float2 ds = *(const float2 *)(rp + 32);                                                    \
         int acc;                                                                                         \
@@ -538,7 +566,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     }
 
     int c0 = 0, um = 0;  // um: record of the chunk's first block column
-    const int ustep = CHUNK / R % nb;
+    const int ustep = (CHUNK >> lgR) % nb;
     for (; c0 + D < nch; c0 += D) {
 #pragma unroll
         for (int j = 0; j < D; j++) {
@@ -564,24 +592,21 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     for (int i0 = 0; i0 < rows_w; i0 += NT) {
         const int i = i0 + tid;
         if (i0 + (tid & ~63) >= rows_w) break;  // the whole wave is past the range
-        const int tl = i / R, r = i % R, tile = t0 + tl;
+        const int tl = i >> lgR, r = i & (R - 1), tile = t0 + tl;
         const int row = R >= 2 * QMH_TILE_R ? tile * (R / 2) + (r & (R / 2 - 1)) : tile * R + r;
         const bool mine = i < rows_w;
         if (i0 > 0 && mine) ein = epi_fetch(a, row, pos);
         float y = 0.0f;
         if (mine) {
             const float *tp = T + (size_t)tl * TB + r;
-            int b = 0;
-            for (; b + 32 <= nb; b += 32) {
-                float v[32];
-#pragma unroll
-                for (int k = 0; k < 32; k++) v[k] = tp[(b + k) * R];
-#pragma unroll
-                for (int k = 0; k < 32; k++) y = y + v[k];
+            switch (R) {  // the terms' stride as an immediate (paired LDS reads with offsets)
+            case 8: y = mv_chain<8>(tp, nb); break;
+            case 16: y = mv_chain<16>(tp, nb); break;
+            case 32: y = mv_chain<32>(tp, nb); break;
+            default: y = mv_chain<64>(tp, nb); break;
             }
-            for (; b < nb; b++) y = y + tp[b * R];
         }
-        mv_epilogue<R>(a, mine ? row : a.rows, y, r, pos, ein, etab);
+        mv_epilogue(a, mine ? row : a.rows, y, r, R >> 1, pos, ein, etab);
     }
 }
 
@@ -620,7 +645,7 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
     for (int i = 0; i < n; i++) s = s + w[i] * xs[i];
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
     const EpiIn e = epi_fetch(a, row, pos);
-    mv_epilogue<QMH_TILE_R * 2>(a, row, s, threadIdx.x & 15, pos, e, qmh_exp2_tab);
+    mv_epilogue(a, row, s, threadIdx.x & 15, QMH_TILE_R, pos, e, qmh_exp2_tab);
 }
 
 extern "C" int qmh_matvec_max_cols(int norm) {
@@ -643,6 +668,8 @@ extern "C" int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int wa
 
 extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     const bool norm = a->norm_w != NULL, image = a->xq_in != NULL;
+    if (a->tile_r != 8 && a->tile_r != 16 && a->tile_r != 32 && a->tile_r != 64) return (int)hipErrorInvalidValue;
+    if (a->epi == QMH_EPI_SWIGLU && a->tile_r < 32) return (int)hipErrorInvalidValue;  // interleaved W1|W3 tiles
     if (grid < 1 || grid > a->ntiles || a->cols < 1 || a->cols > qmh_matvec_max_cols(norm) || (norm && image))
         return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
@@ -652,30 +679,11 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
         return (int)hipErrorInvalidValue;
     if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT>::N * QMH_MV_NT * 16) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_EPI_SWIGLU_Q) != (a->tile_r == 64)) return (int)hipErrorInvalidValue;
-    const int am = image ? MV_ACT_IMAGE : norm ? MV_ACT_NORM : MV_ACT;
     hipStream_t s = (hipStream_t)stream;
-#define QMH_MV(WT, R, AM) \
-    hipLaunchKernelGGL((k_matvec<WT, R, AM, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a)
-#define QMH_MV_AM(WT, R)                                                  \
-    if (am == MV_ACT_NORM) QMH_MV(WT, R, MV_ACT_NORM);                    \
-    else if (am == MV_ACT_IMAGE) QMH_MV(WT, R, MV_ACT_IMAGE);             \
-    else QMH_MV(WT, R, MV_ACT);
-#define QMH_MV_R(WT)                                                      \
-    switch (a->tile_r) {                                                   \
-    case 8: QMH_MV_AM(WT, 8); break;                                      \
-    case 16: QMH_MV_AM(WT, 16); break;                                    \
-    case 32: QMH_MV_AM(WT, 32); break;                                    \
-    case 64: QMH_MV_AM(WT, 64); break;                                    \
-    default: return (int)hipErrorInvalidValue;                             \
-    }
-    if (a->dtype == QMH_Q4) {
-        QMH_MV_R(QMH_Q4);
-    } else {
-        QMH_MV_R(QMH_Q8);
-    }
-#undef QMH_MV_R
-#undef QMH_MV_AM
-#undef QMH_MVS
+    if (a->dtype == QMH_Q4)
+        hipLaunchKernelGGL((k_matvec<QMH_Q4, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a);
+    else
+        hipLaunchKernelGGL((k_matvec<QMH_Q8, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a);
     return (int)hipGetLastError();
 }
 

@@ -64,6 +64,23 @@ def rmsnorm_boundary_input(n: int, eps: float, seed: int, target: float = 0.73) 
     return np.concatenate([bulk, np.array(tail, np.float32)])
 
 
+def rmsnorm_offset_input(n: int, eps: float, seed: int, rel: float, target: float = 0.73) -> np.ndarray:
+    """x[n] (n >= 4) whose 1/sqrt(sum/n + eps) sits at (1 + rel) times a float midpoint: just
+    outside (or inside) the device's margin for taking the float without the exact double chain."""
+    rng = np.random.default_rng(seed)
+    m = _midpoint(np.float32(target * (1.0 + 0.01 * rng.random()))) * (1.0 + rel)
+    ss_t = n * (1.0 / (m * m) - float(np.float32(eps)))
+    bulk = rng.standard_normal(n - 3)
+    bulk = (bulk * math.sqrt(0.5 * ss_t / float(np.sum(bulk * bulk)))).astype(np.float32)
+    p = serial_sum(bulk.astype(np.float64) ** 2)
+    tail = []
+    for _ in range(3):
+        a = _largest_float_sq_at_most(max(ss_t - p, 0.0))
+        tail.append(a)
+        p = p + float(a) * float(a)
+    return np.concatenate([bulk, np.array(tail, np.float32)])
+
+
 def softmax_boundary_input(n: int, seed: int) -> np.ndarray:
     """s[n] (n >= 4), max 0, with (float)(1/sum expf(s_i)) within ~2^-45 of a float midpoint."""
     rng = np.random.default_rng(seed)

@@ -226,6 +226,34 @@ def test_rmsnorm_matvec_boundary_and_random(gpu, oracle, dtype, n):
         L.qmh_weight_free(h)
 
 
+@pytest.mark.parametrize("n", [64, 4096])
+def test_rmsnorm_matvec_near_margin(gpu, oracle, n):
+    """The prologue's inverse RMS without the exact double chain (v_rsq_f64, Newton steps, margin
+    test): inputs whose 1/sqrt(ss/n + eps) sits 2^-44 .. 2^-36 (relative) from a float midpoint,
+    either side, i.e. just outside and inside the margin (2^-40.7 at n = 4096, 2^-45.3 at 64)."""
+    from _boundary import rmsnorm_offset_input
+
+    L = gpu.load_library()
+    rows = 64
+    W = (rng.standard_normal((rows, n)) * 0.05).astype(np.float32)
+    Wq = oracle.quantize(Q8_0, W)
+    h = L.qmh_weight_upload(Q8_0, rows, n, np.ascontiguousarray(Wq).ctypes.data)
+    assert h, gpu.last_error()
+    try:
+        for e in (44, 42, 40, 38, 36):
+            for sign in (1.0, -1.0):
+                for seed in range(2):
+                    x = rmsnorm_offset_input(n, 1e-5, seed, sign * 2.0 ** -e)
+                    g = np.ones(n, np.float32)
+                    want, _ = oracle.matvec(Q8_0, Wq, rows, n, oracle.rmsnorm(x, g, 1e-5))
+                    dx, dg, dy = dev(gpu, x), dev(gpu, g), gpu.DeviceBuffer(rows * 4)
+                    dq = gpu.DeviceBuffer(nblocks(n) * 34)
+                    gpu._check(L.qmh_rmsnorm_matvec(h, dx.ptr, dg.ptr, 1e-5, dy.ptr, dq.ptr, None), "rmsnorm_matvec")
+                    assert np.array_equal(bits(dy.to_array(np.float32)), bits(want)), (n, e, sign, seed)
+    finally:
+        L.qmh_weight_free(h)
+
+
 @pytest.mark.parametrize("n", [7, 64, 512, 4096])
 def test_softmax_boundary(gpu, oracle, n):
     from _boundary import softmax_boundary_input
