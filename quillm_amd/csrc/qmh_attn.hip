@@ -289,15 +289,16 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_heads;
     const float *s0 = att + (size_t)h * max_seq;
-    // loads: the head's scores, then the V float4s (position k*64 + tid/4, columns c .. c+3;
-    // columns past hd re-read the last whole float4 and are never stored)
+    // loads: expf's table (oldest, so storing it to LDS below waits for nothing else), the head's
+    // scores, then the V float4s (position k*64 + tid/4, columns c .. c+3; columns past hd
+    // re-read the last whole float4 and are never stored)
+    const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
     float sv[SK];
 #pragma unroll
     for (int k = 0; k < SK; k++) {
         const int t = tid + k * QMH_WG;
         sv[k] = s0[t < n ? t : 0];
     }
-    qmh_exp_tab_fill(etab);  // published by the max's barrier
     const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
     float4 vv[L4];
 #pragma unroll
@@ -307,6 +308,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     }
     // softmax statistics (src/ops.c:100-112): max (NaN never wins; a NaN at x[0] stays),
     // e_t = expf(x_t - max) kept in P, the double sum as a tree checked against the serial order
+    if (tid < 32) etab[tid] = etv;  // published by the max's barrier
     float m = -__builtin_inff();
 #pragma unroll
     for (int k = 0; k < SK; k++)

@@ -61,8 +61,8 @@ __constant__ static const uint64_t qmh_exp2_tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-// tab: the 32 entries of qmh_exp2_tab, wherever they are (a workgroup may keep a copy in LDS,
-// filled by qmh_exp_tab_fill before a barrier, to take the table lookup off global memory)
+// tab: the 32 entries of qmh_exp2_tab, wherever they are (a workgroup may keep a copy in LDS, to
+// take the table lookup off global memory)
 __device__ __forceinline__ float qmh_expf_t(float x, const uint64_t *tab) {
     uint32_t ux = __float_as_uint(x);
     uint32_t abstop = (ux >> 20) & 0x7ffu;
@@ -91,11 +91,6 @@ __device__ __forceinline__ float qmh_expf_t(float x, const uint64_t *tab) {
     return (float)y;
 }
 __device__ __forceinline__ float qmh_expf(float x) { return qmh_expf_t(x, qmh_exp2_tab); }
-// threads 0..31 copy the table to dst (LDS); visible to the workgroup after the next barrier
-__device__ __forceinline__ void qmh_exp_tab_fill(uint64_t *dst) {
-    if (threadIdx.x < 32) dst[threadIdx.x] = qmh_exp2_tab[threadIdx.x];
-}
-
 // --------------------------------------------------------------------------- reductions
 
 __device__ __forceinline__ float qmh_wave_max(float v) {

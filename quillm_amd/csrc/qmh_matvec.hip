@@ -465,7 +465,11 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
         act_load<false, NT>(a, xr, wr);
     }
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
-    if (a.epi == QMH_EPI_SWIGLU || a.epi == QMH_EPI_SWIGLU_Q) qmh_exp_tab_fill(etab);  // read after the barriers below
+    // expf's table for the SwiGLU epilogues: loaded now, stored to LDS after the stream (a store
+    // here would wait for every load issued so far, the activation's included)
+    const bool swiglu = a.epi == QMH_EPI_SWIGLU || a.epi == QMH_EPI_SWIGLU_Q;
+    uint64_t etv = 0;
+    if (swiglu && tid < 32) etv = qmh_exp2_tab[tid];
 
     // 2. the first D chunks. Each load's resource starts at its own 256 slots and holds what is
     // left of the range, so the range check (on the lane's offset) zeroes slots past the range
@@ -585,6 +589,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
         }
 #undef MV_COMPUTE
 #undef MV_LOAD
+    if (swiglu && tid < 32) etab[tid] = etv;
     __syncthreads();
 
     // 5. serial chains (row i of the range: tile i/R, row i%R; its terms at (tile*nb + b)*R + i%R)
