@@ -137,6 +137,38 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
  * No host round trip between steps. */
 int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
 
+/* ------------------------------------------------------------------ sampler */
+
+/* qm_sampler (src/sampler.h:8-16): temperature / top-k / top-p sampling with an xorshift64*
+ * stream. Results are token for token and rng state for rng state those of the reference's
+ * qm_sample on the same logits (its float and double roundings included). */
+typedef struct qmh_sampler qmh_sampler;
+
+/* qm_sampler_init (src/sampler.c:6-16): the same normalisation (temperature < 0 -> 0, top_k < 0
+ * -> 0, top_p outside (0, 1] -> 1, seed 0 -> 0x9e3779b97f4a7c15); device scratch replaces the
+ * arena arrays. n_vocab in [1, 2^24]. NULL on error. */
+qmh_sampler *qmh_sampler_create(int32_t n_vocab, float temperature, int top_k, float top_p, uint64_t seed);
+void qmh_sampler_free(qmh_sampler *s);
+/* qm_sample (src/sampler.c:50-106) of device logits[n_vocab]: the token is written to device
+ * memory *out, asynchronously on the stream. Greedy configurations (temperature 0 or top_k 1)
+ * take the first argmax and leave the rng alone, as the reference does. */
+int qmh_sample(qmh_sampler *s, const float *logits, int32_t *out, void *stream);
+/* qmh_sample on the library stream, synchronously: the token, or -1 on error. */
+int32_t qmh_sample_sync(qmh_sampler *s, const float *logits);
+/* The rng state (qm_sampler.rng) after the library stream's work. */
+int qmh_sampler_rng(const qmh_sampler *s, uint64_t *state);
+/* Diagnostics of the last non-greedy draw (no reference counterpart): diag[0] the serial double
+ * sum of the exponentials, [1] 0 when every chunk replay agreed, [2] chunks replayed serially
+ * for that sum, [3] candidates, [4] k, [5] nucleus size m, [6] chunks replayed for the nucleus
+ * sum, [7] nucleus mass. probs (NULL or host [n_vocab]): the normalised probabilities. */
+int qmh_sampler_diag(const qmh_sampler *s, double diag[8], float *probs);
+
+/* Sampled decode on the device: n_steps forwards starting with token at pos, each next token
+ * qm_sample of the previous logits (the generation loop of src/main.c:131-141). out[k] receives
+ * the token sampled from the logits at position pos+k. No host round trip between steps. EOS does
+ * not stop the loop (the reference stops there: cut out[] at the first EOS for its output). */
+int qmh_model_sample(qmh_model *m, qmh_sampler *s, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
+
 /* ------------------------------------------------------------------ measurement
  * No reference counterpart (the reference times with a host clock, bench/bench.c:11-38).
  * Stages of one decode step: 0 = fused RMSNorm+QKV matvec (+RoPE, KV write), 1 = Wo matvec

@@ -23,6 +23,10 @@
  *   or_rmsnorm..swiglu   bit-exact against the compiled reference, plus the closed forms of
  *                        tests/test_kernels.c:104-138.
  *   or_argmax            KAT of tests/test_sampler.c:8-12.
+ *   or_sample            token sequences and rng states identical to the compiled reference's
+ *                        qm_sample on seeded logits (every parameter path, NaN/inf logits,
+ *                        ties), the KATs of tests/test_sampler.c, and its distribution checks
+ *                        against softmax(logits/T) in float64.
  *   or_model_forward     bit-exact logits against the compiled reference's qm_model_forward
  *                        (scalar ISA) on generated .qlm files; causality.
  */
@@ -62,6 +66,20 @@ void or_softmax(float *x, int64_t n);
 void or_rope(float *v, int64_t n_heads, int64_t head_dim, int64_t pos, float theta);
 void or_swiglu(float *gate, const float *up, int64_t n);
 int32_t or_argmax(const float *x, int32_t n);
+
+/* ---- sampler (reference src/sampler.{h,c}) ---- */
+typedef struct {
+    float temperature;
+    int top_k;
+    float top_p;
+    uint64_t rng;
+    int32_t n_vocab;
+} or_sampler;
+void or_sampler_init(or_sampler *s, int32_t n_vocab, float temperature, int top_k, float top_p, uint64_t seed);
+float or_rng_uniform(uint64_t *state);
+/* q[n], order[n]: caller's work space (q ends as the normalised probabilities, order as the
+ * sorted candidates); *sum_out (optional) gets the serial double sum of the exponentials. */
+int32_t or_sample(or_sampler *s, const float *logits, float *q, int32_t *order, double *sum_out);
 
 /* ---- model (reference src/model.{h,c}) ---- */
 typedef struct or_model or_model;

@@ -1,6 +1,7 @@
 /* CPU oracle, numerics part -- TEST INFRASTRUCTURE ONLY (see oracle.h).
  * Restates the reference's scalar arithmetic; each function cites what it follows. */
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "oracle.h"
@@ -282,4 +283,93 @@ int32_t or_argmax(const float *x, int32_t n) {
     for (int32_t i = 1; i < n; i++)
         if (x[i] > x[best]) best = i;
     return best;
+}
+
+/* ---- sampler (reference src/sampler.c) ----
+ *
+ * Restated from the algorithm's definition rather than its heap: the reference keeps a size-k
+ * min-heap under less(a,b) = p[a] < p[b] || (p[a] == p[b] && a > b) and heap-sorts it
+ * (src/sampler.c:34-87). Without NaNs that order is total on distinct indices, so the heap's
+ * output is exactly the k largest candidates sorted by (probability descending, index
+ * ascending), which is what a comparison sort with that key yields here. With a NaN
+ * probability the reference's serial double sum is NaN, every probability becomes NaN, less()
+ * is always false, the heap never moves and the first heap-sort swap parks index 0 at position
+ * k-1, which is returned (cum and u are NaN, so no earlier return): token 0. */
+void or_sampler_init(or_sampler *s, int32_t n_vocab, float temperature, int top_k, float top_p, uint64_t seed) {
+    /* parameter normalisation of src/sampler.c:8-12 */
+    s->temperature = temperature < 0 ? 0 : temperature;
+    s->top_k = top_k < 0 ? 0 : top_k;
+    s->top_p = (top_p <= 0 || top_p > 1) ? 1.0f : top_p;
+    s->rng = seed ? seed : 0x9e3779b97f4a7c15ULL;
+    s->n_vocab = n_vocab;
+}
+
+/* xorshift64* (src/sampler.c:18-25): 24 high bits of the scrambled state over 2^24 */
+float or_rng_uniform(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    const uint64_t top24 = (x * 0x2545F4914F6CDD1DULL) >> 40;
+    return (float)top24 / 16777216.0f;
+}
+
+static const float *g_sort_q;
+static int cmp_desc(const void *pa, const void *pb) {
+    const int32_t a = *(const int32_t *)pa, b = *(const int32_t *)pb;
+    const float qa = g_sort_q[a], qb = g_sort_q[b];
+    if (qa != qb) return qa > qb ? -1 : 1;
+    return a < b ? -1 : (a > b);
+}
+
+int32_t or_sample(or_sampler *s, const float *logits, float *q, int32_t *order, double *sum_out) {
+    const int32_t n = s->n_vocab;
+    if (s->temperature == 0.0f || s->top_k == 1) return or_argmax(logits, n); /* src/sampler.c:52 */
+    /* max by a strict-greater scan from logits[0] (src/sampler.c:54-56) */
+    float mx = logits[0];
+    for (int32_t i = 1; i < n; i++)
+        if (logits[i] > mx) mx = logits[i];
+    /* exponentials as floats, summed in index order in double (src/sampler.c:57-61) */
+    double sum = 0;
+    for (int32_t i = 0; i < n; i++) {
+        q[i] = expf((logits[i] - mx) / s->temperature);
+        sum += q[i];
+    }
+    if (sum_out) *sum_out = sum;
+    for (int32_t i = 0; i < n; i++) q[i] = (float)(q[i] / sum); /* src/sampler.c:62 */
+    const float u01 = or_rng_uniform(&s->rng);                 /* drawn once per non-greedy call */
+    if (sum != sum) return 0;                                   /* NaN: see the header comment */
+    /* candidates (src/sampler.c:64-75): the top-p prefilter, or every index */
+    int32_t nc = 0;
+    if (s->top_k == 0 && s->top_p < 1.0f && n > 1) {
+        const float cut = (1.0f - s->top_p) / (float)(n - 1);
+        for (int32_t i = 0; i < n; i++)
+            if (q[i] >= cut) order[nc++] = i;
+    }
+    if (nc == 0)
+        for (int32_t i = 0; i < n; i++) order[nc++] = i;
+    const int32_t k = (s->top_k > 0 && s->top_k < nc) ? s->top_k : nc;
+    g_sort_q = q;
+    qsort(order, (size_t)nc, sizeof(int32_t), cmp_desc);
+    /* nucleus: the shortest prefix whose serial double sum reaches top_p (src/sampler.c:89-99) */
+    double cum = 0;
+    int32_t m = k;
+    for (int32_t i = 0; i < k; i++) {
+        cum += q[order[i]];
+        if (cum >= s->top_p) {
+            m = i + 1;
+            break;
+        }
+    }
+    double mass = 0;
+    for (int32_t i = 0; i < m; i++) mass += q[order[i]];
+    /* inverse-CDF draw over the nucleus (src/sampler.c:100-105) */
+    const double u = (double)u01 * mass;
+    double c = 0;
+    for (int32_t i = 0; i < m; i++) {
+        c += q[order[i]];
+        if (u < c) return order[i];
+    }
+    return order[m - 1];
 }

@@ -90,6 +90,13 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_model_forward": (ctypes.POINTER(ctypes.c_float), [vp, i32, i32]),
         "qmh_model_prefill": (ctypes.c_int, [vp, vp, i32, i32, vp]),
         "qmh_model_greedy": (ctypes.c_int, [vp, i32, i32, i32, vp]),
+        "qmh_sampler_create": (vp, [i32, f32, ctypes.c_int, f32, ctypes.c_uint64]),
+        "qmh_sampler_free": (None, [vp]),
+        "qmh_sample": (ctypes.c_int, [vp, vp, vp, vp]),
+        "qmh_sample_sync": (i32, [vp, vp]),
+        "qmh_sampler_rng": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64)]),
+        "qmh_sampler_diag": (ctypes.c_int, [vp, vp, vp]),
+        "qmh_model_sample": (ctypes.c_int, [vp, vp, i32, i32, i32, vp]),
         "qmh_gen_qlm": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(QmhConfig), ctypes.c_int, ctypes.c_uint64,
                                        ctypes.c_int]),
         "qmh_gen_values": (None, [ctypes.c_uint64, ctypes.c_int, i64, i64, vp]),
@@ -209,6 +216,13 @@ class Model:
                "greedy")
         return out[:n_steps]
 
+    def sample(self, sampler: "Sampler", token: int, pos: int, n_steps: int) -> np.ndarray:
+        """Sampled decode on the device (qmh_model_sample): the n_steps sampled tokens."""
+        out = np.zeros(max(n_steps, 1), np.int32)
+        _check(load_library().qmh_model_sample(self._h, sampler._h, int(token), int(pos), int(n_steps),
+                                                out.ctypes.data), "model_sample")
+        return out[:n_steps]
+
     STAGES = {"qkv": 0, "wo": 1, "w13": 2, "w2": 3, "output": 4, "attn_scores": 5, "attn_pv": 6}
 
     def time_stage(self, stage: str, iters: int, pos: int):
@@ -229,6 +243,66 @@ class Model:
     def close(self):
         if self._h:
             load_library().qmh_model_free(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ----------------------------------------------------------------------------- sampler
+
+class Sampler:
+    """Device sampler: the HIP counterpart of the reference's qm_sampler (src/sampler.h:8-24)."""
+
+    def __init__(self, n_vocab: int, temperature: float, top_k: int, top_p: float, seed: int):
+        self.n = int(n_vocab)
+        self._h = load_library().qmh_sampler_create(self.n, float(temperature), int(top_k), float(top_p),
+                                                     int(seed) & (2**64 - 1))
+        if not self._h:
+            raise QmhError(f"qmh_sampler_create: {last_error()}")
+        self._logits = DeviceBuffer(4 * self.n)
+
+    def sample(self, logits) -> int:
+        """qm_sample of host logits (uploaded) or of a DeviceBuffer holding n floats."""
+        if isinstance(logits, DeviceBuffer):
+            ptr = logits.ptr
+        else:
+            lg = np.ascontiguousarray(logits, np.float32)
+            if lg.size != self.n:
+                raise ValueError(f"logits of {lg.size} values for a vocabulary of {self.n}")
+            _check(load_library().qmh_memcpy_h2d(self._logits.ptr, lg.ctypes.data, 4 * self.n), "h2d")
+            ptr = self._logits.ptr
+        tok = load_library().qmh_sample_sync(self._h, ptr)
+        if tok < 0:
+            raise QmhError(f"qmh_sample: {last_error()}")
+        return int(tok)
+
+    @property
+    def rng(self) -> int:
+        st = ctypes.c_uint64()
+        _check(load_library().qmh_sampler_rng(self._h, ctypes.byref(st)), "sampler_rng")
+        return int(st.value)
+
+    def diag(self, probs: bool = False):
+        """(diag[8], probabilities or None) of the last non-greedy draw."""
+        d = np.zeros(8, np.float64)
+        q = np.zeros(self.n, np.float32) if probs else None
+        _check(load_library().qmh_sampler_diag(self._h, d.ctypes.data, q.ctypes.data if probs else None),
+               "sampler_diag")
+        return d, q
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load_library().qmh_sampler_free(self._h)
             self._h = None
 
     def __enter__(self):

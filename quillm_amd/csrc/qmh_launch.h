@@ -114,6 +114,29 @@ int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, flo
  * record[step] = idx (when step < record_cap) where step = tokpos[2]++ (device greedy loop state) */
 int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record, int record_cap,
                       void *stream);
+/* one qm_sample (src/sampler.c:50-106) of a non-greedy sampler: token -> *out (and the decode
+ * loop's tokpos/record like qmh_launch_argmax); rng advanced in place. p: [n] scratch (ends as the
+ * probabilities), key0/key1/idx0/idx1: [n] sort scratch; diag (optional, [8]): serial sum, status
+ * (0 = every replayed chunk end matched), chunks replayed, candidates, k, m, chunks replayed in
+ * the nucleus sum, nucleus mass. */
+typedef struct {
+    const float *logits;
+    int n;
+    float temperature;
+    int top_k;
+    float top_p;
+    uint64_t *rng;
+    float *p;
+    uint32_t *key0, *key1;
+    int32_t *idx0, *idx1;
+    int32_t *out;
+    int32_t *tokpos;
+    int32_t *record;
+    int record_cap;
+    double *diag;
+} qmh_sample_args;
+int qmh_launch_sample(const qmh_sample_args *a, void *stream);
+
 /* gate = silu(gate)*up over n (src/ops.c:128-133) */
 int qmh_launch_swiglu(float *gate, const float *up, int64_t n, void *stream);
 

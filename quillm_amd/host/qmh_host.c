@@ -964,6 +964,150 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
     return 0;
 }
 
+/* ------------------------------------------------------------------ sampler */
+
+/* qm_sampler (src/sampler.h:8-16) with its two arena arrays replaced by device scratch: the
+ * exponentials / probabilities and the radix-sort key and index buffers. The rng state lives on
+ * the device, so sampling never returns to the host. */
+struct qmh_sampler {
+    int32_t n_vocab;
+    float temperature, top_p;
+    int top_k;
+    uint64_t *d_rng;
+    double *d_diag;
+    int32_t *d_out;
+    float *d_p;
+    uint32_t *d_key[2];
+    int32_t *d_idx[2];
+};
+
+/* the reference's greedy shortcut (src/sampler.c:52): no draw, the rng is left alone */
+static int sampler_greedy(const qmh_sampler *s) { return s->temperature == 0.0f || s->top_k == 1; }
+
+void qmh_sampler_free(qmh_sampler *s) {
+    if (!s) return;
+    void *bufs[] = {s->d_rng, s->d_diag, s->d_out, s->d_p, s->d_key[0], s->d_key[1], s->d_idx[0], s->d_idx[1]};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
+        if (bufs[i]) hipFree(bufs[i]);
+    free(s);
+}
+
+qmh_sampler *qmh_sampler_create(int32_t n_vocab, float temperature, int top_k, float top_p, uint64_t seed) {
+    if (ensure()) return NULL;
+    if (n_vocab < 1 || n_vocab > (1 << 24)) {
+        fail("sampler: n_vocab %d outside [1, 2^24]", (int)n_vocab);
+        return NULL;
+    }
+    qmh_sampler *s = calloc(1, sizeof *s);
+    if (!s) {
+        fail("sampler: out of host memory");
+        return NULL;
+    }
+    /* parameter normalisation of qm_sampler_init (src/sampler.c:8-12) */
+    s->n_vocab = n_vocab;
+    s->temperature = temperature < 0 ? 0 : temperature;
+    s->top_k = top_k < 0 ? 0 : top_k;
+    s->top_p = (top_p <= 0 || top_p > 1) ? 1.0f : top_p;
+    uint64_t rng = seed ? seed : 0x9e3779b97f4a7c15ULL;
+    const size_t n = (size_t)n_vocab;
+    hipError_t e = hipMalloc((void **)&s->d_rng, sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&s->d_diag, 8 * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc((void **)&s->d_out, sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&s->d_p, n * sizeof(float));
+    for (int k = 0; k < 2 && e == hipSuccess; k++) {
+        e = hipMalloc((void **)&s->d_key[k], n * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMalloc((void **)&s->d_idx[k], n * sizeof(int32_t));
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(s->d_rng, &rng, sizeof rng, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        fail("sampler: %s", hipGetErrorString(e));
+        qmh_sampler_free(s);
+        return NULL;
+    }
+    return s;
+}
+
+static qmh_sample_args sample_args(const qmh_sampler *s, const float *logits) {
+    qmh_sample_args a;
+    memset(&a, 0, sizeof a);
+    a.logits = logits;
+    a.n = s->n_vocab;
+    a.temperature = s->temperature;
+    a.top_k = s->top_k;
+    a.top_p = s->top_p;
+    a.rng = s->d_rng;
+    a.p = s->d_p;
+    a.key0 = s->d_key[0];
+    a.key1 = s->d_key[1];
+    a.idx0 = s->d_idx[0];
+    a.idx1 = s->d_idx[1];
+    a.diag = s->d_diag;
+    return a;
+}
+
+int qmh_sample(qmh_sampler *s, const float *logits, int32_t *out, void *stream) {
+    if (ensure()) return -1;
+    if (!s || !logits || !out) return fail("sample: NULL argument");
+    if (sampler_greedy(s)) {
+        LCHK(qmh_launch_argmax(logits, s->n_vocab, out, NULL, NULL, 0, S(stream)));
+        return 0;
+    }
+    qmh_sample_args a = sample_args(s, logits);
+    a.out = out;
+    LCHK(qmh_launch_sample(&a, S(stream)));
+    return 0;
+}
+
+int32_t qmh_sample_sync(qmh_sampler *s, const float *logits) {
+    if (!s) return fail("sample: NULL sampler");
+    if (qmh_sample(s, logits, s->d_out, NULL)) return -1;
+    int32_t tok = -1;
+    HIPCHK(hipMemcpyAsync(&tok, s->d_out, sizeof tok, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return tok;
+}
+
+int qmh_sampler_rng(const qmh_sampler *s, uint64_t *state) {
+    if (!s || !state) return fail("sampler_rng: NULL argument");
+    HIPCHK(hipMemcpyAsync(state, s->d_rng, sizeof *state, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int qmh_sampler_diag(const qmh_sampler *s, double diag[8], float *probs) {
+    if (!s || !diag) return fail("sampler_diag: NULL argument");
+    HIPCHK(hipMemcpyAsync(diag, s->d_diag, 8 * sizeof(double), hipMemcpyDeviceToHost, g_stream));
+    if (probs)
+        HIPCHK(hipMemcpyAsync(probs, s->d_p, sizeof(float) * (size_t)s->n_vocab, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int qmh_model_sample(qmh_model *m, qmh_sampler *s, int32_t token, int32_t pos, int32_t n_steps, int32_t *out) {
+    if (!m || !s) return fail("model_sample: NULL argument");
+    if (s->n_vocab != m->cfg.vocab_size)
+        return fail("model_sample: sampler vocab %d != model vocab %d", (int)s->n_vocab, (int)m->cfg.vocab_size);
+    if (sampler_greedy(s)) return qmh_model_greedy(m, token, pos, n_steps, out);
+    if (n_steps < 0 || token < 0 || token >= m->cfg.vocab_size || pos < 0 || (int64_t)pos + n_steps > m->cfg.max_seq)
+        return fail("model_sample: bad token/range");
+    int32_t *slot = m->h_tokpos;
+    slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
+    HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream));
+    qmh_sample_args a = sample_args(s, m->d_logits);
+    a.tokpos = m->d_tokpos;
+    a.record = m->d_record;
+    a.record_cap = m->cfg.max_seq;
+    for (int32_t k = 0; k < n_steps; k++) {
+        HIPCHK(run_step(m, 0));
+        LCHK(qmh_launch_sample(&a, g_stream));
+    }
+    if (n_steps > 0 && out)
+        HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
 /* ------------------------------------------------------------------ generator */
 
 int qmh_gen_qlm(const char *path, const qmh_config *cfg, int wtype, uint64_t seed, int n_threads) {

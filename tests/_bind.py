@@ -62,6 +62,9 @@ class Oracle:
             "or_rope": (None, [vp, i64, i64, i64, f32]),
             "or_swiglu": (None, [vp, vp, i64]),
             "or_argmax": (i32, [vp, i32]),
+            "or_sampler_init": (None, [vp, i32, f32, ctypes.c_int, f32, ctypes.c_uint64]),
+            "or_rng_uniform": (f32, [vp]),
+            "or_sample": (i32, [vp, vp, vp, vp, vp]),
             "or_model_load": (vp, [ctypes.c_char_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]),
             "or_model_free": (None, [vp]),
             "or_model_forward": (ctypes.POINTER(f32), [vp, i32, i32]),
@@ -143,6 +146,10 @@ class Oracle:
     def argmax(self, x):
         return self.L.or_argmax(_ptr(x), x.size)
 
+    # sampler
+    def sampler(self, n_vocab, temperature, top_k, top_p, seed):
+        return OracleSampler(self, n_vocab, temperature, top_k, top_p, seed)
+
     # model
     def run_model(self, path: str, prompt, n_gen: int, max_seq: int = 0, keep_logits=True):
         """P forwards over prompt then n_gen greedy steps; returns (logits [P+n_gen, V] or None, ids)."""
@@ -178,6 +185,35 @@ class Oracle:
         return m
 
 
+class OrSampler(ctypes.Structure):
+    """oracle/oracle.h or_sampler."""
+
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int), ("top_p", ctypes.c_float),
+                ("rng", ctypes.c_uint64), ("n_vocab", ctypes.c_int32)]
+
+
+class OracleSampler:
+    """A seeded oracle sampler: sample(logits) -> token; q / total of the last call kept."""
+
+    def __init__(self, oracle, n_vocab, temperature, top_k, top_p, seed):
+        self.o, self.n = oracle, n_vocab
+        self.st = OrSampler()
+        oracle.L.or_sampler_init(ctypes.byref(self.st), n_vocab, temperature, top_k, top_p, seed)
+        self.q = np.zeros(n_vocab, np.float32)
+        self.order = np.zeros(n_vocab, np.int32)
+        self.total = ctypes.c_double(0.0)
+
+    @property
+    def rng(self):
+        return int(self.st.rng)
+
+    def sample(self, logits) -> int:
+        lg = np.ascontiguousarray(logits, np.float32)
+        assert lg.size == self.n
+        return int(self.o.L.or_sample(ctypes.byref(self.st), _ptr(lg), _ptr(self.q), _ptr(self.order),
+                                      ctypes.byref(self.total)))
+
+
 class QmTensor(ctypes.Structure):
     """The reference's qm_tensor (src/ops.h:9-15)."""
 
@@ -207,6 +243,12 @@ class Ref:
             "qm_rope": (None, [vp, i64, i64, i64, f32]),
             "qm_swiglu": (None, [vp, vp, i64]),
             "qm_argmax": (i32, [vp, i32]),
+            "qm_arena_init": (ctypes.c_int, [vp, ctypes.c_size_t]),
+            "qm_arena_reset": (None, [vp]),
+            "qm_arena_free": (None, [vp]),
+            "qm_sampler_init": (ctypes.c_int, [vp, vp, i32, f32, ctypes.c_int, f32, ctypes.c_uint64]),
+            "qm_sample": (i32, [vp, vp]),
+            "qm_rng_uniform": (f32, [vp]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -242,6 +284,48 @@ class Ref:
         xq = np.zeros(nblocks(cols) * 34, np.uint8)
         self.L.qm_matvec(None, ctypes.byref(t), _ptr(x), _ptr(y), _ptr(xq))
         return y, xq
+
+
+class QmArena(ctypes.Structure):
+    """The reference's qm_arena (src/qm_base.h:49-52)."""
+
+    _fields_ = [("base", ctypes.c_void_p), ("cap", ctypes.c_size_t), ("used", ctypes.c_size_t),
+                ("peak", ctypes.c_size_t)]
+
+
+class QmSampler(ctypes.Structure):
+    """The reference's qm_sampler (src/sampler.h:8-16)."""
+
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int), ("top_p", ctypes.c_float),
+                ("rng", ctypes.c_uint64), ("n_vocab", ctypes.c_int32), ("probs", ctypes.c_void_p),
+                ("idx", ctypes.c_void_p)]
+
+
+class RefSampler:
+    """The compiled reference's own qm_sampler_init / qm_sample, with its arena."""
+
+    def __init__(self, ref, n_vocab, temperature, top_k, top_p, seed):
+        self.r, self.n = ref, n_vocab
+        self.arena = QmArena()
+        assert ref.L.qm_arena_init(ctypes.byref(self.arena), 8 * n_vocab + 4096) == 0
+        self.st = QmSampler()
+        assert ref.L.qm_sampler_init(ctypes.byref(self.st), ctypes.byref(self.arena), n_vocab, temperature, top_k,
+                                     top_p, seed) == 0
+
+    @property
+    def rng(self):
+        return int(self.st.rng)
+
+    def sample(self, logits) -> int:
+        lg = np.ascontiguousarray(logits, np.float32)
+        assert lg.size == self.n
+        return int(self.r.L.qm_sample(ctypes.byref(self.st), _ptr(lg)))
+
+    def __del__(self):
+        try:
+            self.r.L.qm_arena_free(ctypes.byref(self.arena))
+        except Exception:
+            pass
 
 
 def ref_run(model: str, prompt, n_gen: int, isa: str = "scalar", threads: int = 1, max_seq: int = 0,
