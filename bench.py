@@ -162,6 +162,15 @@ def main():
         value = K / (dev_ms / 1e3)
         log(f"[bench] decode {K} steps: {dev_ms:.2f} ms device ({wall_s * 1e3:.2f} ms wall), {value:.1f} tok/s")
 
+        # the same steps sampled on the device with the reference CLI's default sampler
+        # (src/main.c:70-72: temperature 0.8, top-k 0, top-p 0.95, seed 42); wall clock, synchronous
+        with q.Sampler(w.vocab_size, 0.8, 0, 0.95, 42) as smp:
+            m.sample(smp, tok0, P, min(W, 8))
+            t0 = time.perf_counter()
+            m.sample(smp, tok0, P, K)
+            sampled_s = time.perf_counter() - t0
+        log(f"[bench] sampled decode {K} steps: {sampled_s * 1e3:.2f} ms wall, {K / sampled_s:.1f} tok/s")
+
         # dominant kernel: fused RMSNorm + W1|W3 matvec + SwiGLU, cycling the layers
         stages = {}
         for st in ("qkv", "wo", "w13", "w2", "output", "attn_scores", "attn_pv"):
@@ -195,6 +204,7 @@ def main():
                                f"batch 1, prompt {P}, decode {K} greedy",
                    "prompt": P, "decode_steps": K, "max_seq": P + max(K, W)},
         "prefill_tok_s": round(P / prefill_s, 2),
+        "sampled_decode_tok_s": round(K / sampled_s, 2),
         "decode_bytes_per_token": int(bpt),
         "decode_hbm_frac": round(value * bpt / (HBM_PEAK_GBS * 1e9), 4),
         "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),

@@ -134,7 +134,9 @@ typedef struct {
     int32_t *record;
     int record_cap;
     double *diag;
+    void *ws; /* qmh_sample_ws_bytes(n) bytes, zeroed once at allocation (large vocabularies) */
 } qmh_sample_args;
+size_t qmh_sample_ws_bytes(int n);
 int qmh_launch_sample(const qmh_sample_args *a, void *stream);
 
 /* gate = silu(gate)*up over n (src/ops.c:128-133) */

@@ -979,6 +979,7 @@ struct qmh_sampler {
     float *d_p;
     uint32_t *d_key[2];
     int32_t *d_idx[2];
+    void *d_ws; /* control block and chunk arrays of the multi-workgroup path */
 };
 
 /* the reference's greedy shortcut (src/sampler.c:52): no draw, the rng is left alone */
@@ -986,7 +987,8 @@ static int sampler_greedy(const qmh_sampler *s) { return s->temperature == 0.0f 
 
 void qmh_sampler_free(qmh_sampler *s) {
     if (!s) return;
-    void *bufs[] = {s->d_rng, s->d_diag, s->d_out, s->d_p, s->d_key[0], s->d_key[1], s->d_idx[0], s->d_idx[1]};
+    void *bufs[] = {s->d_rng,    s->d_diag,   s->d_out,    s->d_p,   s->d_key[0],
+                    s->d_key[1], s->d_idx[0], s->d_idx[1], s->d_ws};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) hipFree(bufs[i]);
     free(s);
@@ -1018,6 +1020,9 @@ qmh_sampler *qmh_sampler_create(int32_t n_vocab, float temperature, int top_k, f
         e = hipMalloc((void **)&s->d_key[k], n * sizeof(uint32_t));
         if (e == hipSuccess) e = hipMalloc((void **)&s->d_idx[k], n * sizeof(int32_t));
     }
+    const size_t wsb = qmh_sample_ws_bytes(n_vocab);
+    if (e == hipSuccess && wsb) e = hipMalloc(&s->d_ws, wsb);
+    if (e == hipSuccess && wsb) e = hipMemsetAsync(s->d_ws, 0, wsb, g_stream);
     if (e == hipSuccess) e = hipMemcpyAsync(s->d_rng, &rng, sizeof rng, hipMemcpyHostToDevice, g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) {
@@ -1043,6 +1048,7 @@ static qmh_sample_args sample_args(const qmh_sampler *s, const float *logits) {
     a.idx0 = s->d_idx[0];
     a.idx1 = s->d_idx[1];
     a.diag = s->d_diag;
+    a.ws = s->d_ws;
     return a;
 }
 

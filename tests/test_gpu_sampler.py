@@ -72,6 +72,16 @@ def test_sampler_32k(gpu, oracle, ref, cfg):
     check_seq(gpu, oracle, ref, 32000, cfg, 17, seq)
 
 
+@pytest.mark.parametrize("n", [8193, 20000])
+def test_sampler_grid_path_sizes(gpu, oracle, ref, n):
+    # vocabularies above 8192 take the multi-workgroup path: every family and parameter path
+    say("sampler grid path", n)
+    for cfg in [(0.8, 0, 0.95), (1.0, 0, 1.0), (0.7, 40, 0.9), (1.0, 3, 1.0), (1.0, 0, 1e-6), (0.5, 0, 0.5)]:
+        rs = np.random.default_rng(zlib.crc32(repr((n, cfg)).encode()))
+        seq = [logit_family(k, n, rs) for k in ("normal2", "peaky", "flat", "ties", "wide", "zeros")]
+        check_seq(gpu, oracle, ref, n, cfg, 23, seq)
+
+
 def test_sampler_large_vocab(gpu, oracle, ref):
     # a Llama-3-sized vocabulary: 126 elements per chunk
     rs = np.random.default_rng(3)
@@ -102,7 +112,7 @@ def test_sampler_adversarial_sums(gpu, oracle, ref):
 
 def test_sampler_nonfinite(gpu, oracle, ref):
     rs = np.random.default_rng(11)
-    for n in (1, 2, 7, 300, 4096):
+    for n in (1, 2, 7, 300, 4096, 20000):
         base = (rs.standard_normal(n) * 2).astype(np.float32)
         cases = []
         for v in (np.nan, np.inf, -np.inf):
@@ -184,3 +194,18 @@ def test_model_sample_matches_oracle(gpu, oracle, small_models, cfg):
         got = m.sample(s, prompt[-1], len(prompt) - 1, n_gen)
         assert list(got) == want
         assert s.rng == want_rng
+
+
+def test_model_sample_reference_protocol(gpu, oracle, small_models):
+    """tests/test_model.c:104-126: BOS at position 0, qm_sampler_init(0.9, 20, 0.9, 1234), 40 sampled
+    steps on a q8_0 model; the sequence is the oracle's, and a second run repeats it."""
+    path = small_models[("small", "q8_0")]
+    cfg = (0.9, 20, 0.9)
+    # oracle: forward(BOS, 0), then 40 x (sample, forward); the device loop is the same 40 draws
+    want, want_rng = oracle_sampled_run(oracle, path, [0], 40, cfg, 1234)
+    runs = []
+    for _ in range(2):
+        with gpu.Model.load(path) as m, gpu.Sampler(m.vocab, *cfg, 1234) as s:
+            runs.append((list(m.sample(s, 0, 0, 40)), s.rng))
+    assert runs[0] == runs[1]
+    assert runs[0][0] == want and runs[0][1] == want_rng
