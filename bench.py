@@ -208,7 +208,7 @@ def main():
         "decode_bytes_per_token": int(bpt),
         "decode_hbm_frac": round(value * bpt / (HBM_PEAK_GBS * 1e9), 4),
         "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
-        "roofline": {"kernel": "k_matvec<Q4_0,64,NORM> (RMSNorm + W1|W3 + SwiGLU + W2's quantized input)",
+        "roofline": {"kernel": "k_matvec<Q4_0> W1|W3 launch (64-row tiles: RMSNorm + W1|W3 + SwiGLU + W2's quantized input)",
                      "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
