@@ -137,6 +137,25 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
  * No host round trip between steps. */
 int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out);
 
+/* ------------------------------------------------------------------ batched decode (bs > 1) */
+
+/* n_seq independent sequences decoded together over one model's weights (no reference counterpart:
+ * the reference decodes one sequence, src/model.c:158-191). Each sequence has its own KV cache of
+ * the model's max_seq positions, separate from the model's own. Per sequence, logits and KV contents
+ * are bitwise those of the single-sequence qmh_model_forward at the same tokens and positions.
+ * Needs quantized weights and head_dim <= 128; n_seq in [1, min(max_seq, 512)]. NULL on error. */
+typedef struct qmh_batch qmh_batch;
+qmh_batch *qmh_batch_create(qmh_model *m, int32_t n_seq);
+void qmh_batch_free(qmh_batch *b);
+/* One step: sequence i takes tokens[i] at position pos[i] (any mix of positions). logits: NULL, or
+ * host memory for n_seq x vocab floats. Synchronous. 0 or -1. */
+int qmh_batch_forward(qmh_batch *b, const int32_t *tokens, const int32_t *pos, float *logits);
+/* n_steps greedy steps of every sequence on the device, from tokens[i] at pos[i]: out[k*n_seq + i]
+ * is sequence i's argmax after step k (the token it takes at step k+1). ms (optional): device time
+ * of the n_steps steps from HIP events. 0 or -1. */
+int qmh_batch_greedy(qmh_batch *b, const int32_t *tokens, const int32_t *pos, int32_t n_steps, int32_t *out,
+                     double *ms);
+
 /* ------------------------------------------------------------------ sampler */
 
 /* qm_sampler (src/sampler.h:8-16): temperature / top-k / top-p sampling with an xorshift64*

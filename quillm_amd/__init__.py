@@ -90,6 +90,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_model_forward": (ctypes.POINTER(ctypes.c_float), [vp, i32, i32]),
         "qmh_model_prefill": (ctypes.c_int, [vp, vp, i32, i32, vp]),
         "qmh_model_greedy": (ctypes.c_int, [vp, i32, i32, i32, vp]),
+        "qmh_batch_create": (vp, [vp, i32]),
+        "qmh_batch_free": (None, [vp]),
+        "qmh_batch_forward": (ctypes.c_int, [vp, vp, vp, vp]),
+        "qmh_batch_greedy": (ctypes.c_int, [vp, vp, vp, i32, vp, ctypes.POINTER(ctypes.c_double)]),
         "qmh_sampler_create": (vp, [i32, f32, ctypes.c_int, f32, ctypes.c_uint64]),
         "qmh_sampler_free": (None, [vp]),
         "qmh_sample": (ctypes.c_int, [vp, vp, vp, vp]),
@@ -243,6 +247,55 @@ class Model:
     def close(self):
         if self._h:
             load_library().qmh_model_free(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ----------------------------------------------------------------------------- batched decode
+
+class Batch:
+    """n_seq independent sequences decoded together over a Model's weights (qmh_batch_*)."""
+
+    def __init__(self, model: "Model", n_seq: int):
+        self.model, self.n, self.vocab = model, int(n_seq), model.vocab
+        self._h = load_library().qmh_batch_create(model._h, self.n)
+        if not self._h:
+            raise QmhError(f"qmh_batch_create: {last_error()}")
+
+    def forward(self, tokens, pos, want_logits: bool = True):
+        """One step (sequence i takes tokens[i] at pos[i]); logits [n_seq, vocab] or None."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        assert t.size == self.n and p.size == self.n
+        out = np.empty((self.n, self.vocab), np.float32) if want_logits else None
+        _check(load_library().qmh_batch_forward(self._h, t.ctypes.data, p.ctypes.data,
+                                                 out.ctypes.data if out is not None else None), "batch_forward")
+        return out
+
+    def greedy(self, tokens, pos, n_steps: int):
+        """(ids [n_steps, n_seq], device ms) of n_steps device greedy steps of every sequence."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        out = np.zeros((max(n_steps, 1), self.n), np.int32)
+        ms = ctypes.c_double()
+        _check(load_library().qmh_batch_greedy(self._h, t.ctypes.data, p.ctypes.data, int(n_steps), out.ctypes.data,
+                                                ctypes.byref(ms)), "batch_greedy")
+        return out[:n_steps], ms.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load_library().qmh_batch_free(self._h)
             self._h = None
 
     def __enter__(self):

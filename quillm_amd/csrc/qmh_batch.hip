@@ -1,0 +1,173 @@
+// gfx950 attention for batched decode: B independent sequences, one query each, every sequence over
+// its own KV cache up to its own position. Per (sequence, head) the arithmetic is that of the single-
+// sequence decode (src/model.c:127-156): each score is one lane's serial float chain over head_dim
+// times the scale, the softmax is the reference's (src/ops.c:100-112, double sum through the
+// certified tree bound or the serial fallback), and each output element is one lane's chain over
+// positions 0..pos of p_t * v_t[i] from +0. Kept in its own code object so the decode kernels'
+// placement does not move.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmh_device.h"
+#include "qmh_launch.h"
+
+namespace {
+
+// scores of sequence blockIdx.y, head blockIdx.x, positions blockIdx.z*QMH_WG + threadIdx.x
+__global__ __launch_bounds__(QMH_WG) void k_bt_scores(const float *__restrict__ Q, const float *__restrict__ Kt,
+                                                      long long kv_stride, const int32_t *__restrict__ pos_arr,
+                                                      float *att, int n_heads, int n_kv, int hd, int max_seq,
+                                                      float scale) {
+    __shared__ float qs[256];
+    const int h = blockIdx.x, b = blockIdx.y, t = blockIdx.z * QMH_WG + threadIdx.x;
+    const int pos = pos_arr[b];
+    if ((int)blockIdx.z * QMH_WG > pos) return;  // past this sequence's positions
+    const int kvh = h / (n_heads / n_kv), D = n_heads * hd;
+    for (int i = threadIdx.x; i < hd; i += QMH_WG) qs[i] = Q[(size_t)b * D + h * hd + i];
+    __syncthreads();
+    if (t > pos) return;
+    const float *kc = Kt + (size_t)b * kv_stride + (size_t)kvh * hd * max_seq + t;
+    float s = 0.0f;
+    for (int d0 = 0; d0 < hd; d0 += 8) {
+        float kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (d0 + j < hd) s = s + qs[d0 + j] * kv[j];
+    }
+    att[((size_t)b * n_heads + h) * max_seq + t] = s * scale;
+}
+
+// softmax of the row of (sequence blockIdx.y, head blockIdx.x) in place, as the decode kernels
+__global__ __launch_bounds__(QMH_WG) void k_bt_softmax(float *att, const int32_t *__restrict__ pos_arr, int n_heads,
+                                                       int max_seq) {
+    __shared__ double red[16];
+    __shared__ float redf[16];
+    const int h = blockIdx.x, b = blockIdx.y, n = pos_arr[b] + 1;
+    float *x = att + ((size_t)b * n_heads + h) * max_seq;
+    float m = -__builtin_inff();
+    for (int t = threadIdx.x; t < n; t += QMH_WG) m = x[t] > m ? x[t] : m;
+    m = qmh_block_max(m, redf);
+    if (x[0] != x[0]) m = x[0];  // the reference's scan starts from x[0]: a NaN there stays
+    double sum = 0.0;
+    for (int t = threadIdx.x; t < n; t += QMH_WG) {
+        const float e = qmh_expf(x[t] - m);
+        x[t] = e;
+        sum += (double)e;
+    }
+    sum = qmh_block_sum_d(sum, red);
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
+        if (threadIdx.x == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)x[t];
+            red[8] = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(red[8]);
+    }
+    for (int t = threadIdx.x; t < n; t += QMH_WG) x[t] = x[t] * inv;
+}
+
+// out[b][h*hd + i] = +0 + p_0 v_0[i] + ... + p_pos v_pos[i]: thread i runs column i's chain; the
+// probabilities pass through LDS 256 positions at a time, V rows are read 8 positions ahead
+constexpr int BT_PV = 128;
+__global__ __launch_bounds__(BT_PV) void k_bt_pv(const float *__restrict__ att, const float *__restrict__ V,
+                                                 long long kv_stride, const int32_t *__restrict__ pos_arr,
+                                                 float *out, int n_heads, int n_kv, int hd, int max_seq) {
+    __shared__ float ps[256];
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x, n = pos_arr[b] + 1;
+    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv;
+    const float *prow = att + ((size_t)b * n_heads + h) * max_seq;
+    const float *vcol = V + (size_t)b * kv_stride + (size_t)kvh * hd + (i < hd ? i : 0);
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += 256) {
+        const int nt = min(256, n - c0);
+        __syncthreads();
+        for (int k = i; k < nt; k += BT_PV) ps[k] = prow[c0 + k];
+        __syncthreads();
+        for (int t0 = 0; t0 < nt; t0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = vcol[(size_t)(c0 + (t0 + j < nt ? t0 + j : nt - 1)) * kvd];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (t0 + j < nt) acc = acc + ps[t0 + j] * v[j];
+        }
+    }
+    if (i < hd) out[(size_t)b * n_heads * hd + h * hd + i] = acc;
+}
+
+}  // namespace
+
+extern "C" int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride,
+                                       const int32_t *pos, int max_pos, float *att, float *out, int B, int n_heads,
+                                       int n_kv, int hd, int max_seq, float scale, void *stream) {
+    if (B < 1 || hd < 1 || hd > 128 || n_kv < 1 || n_heads % n_kv || max_pos < 0 || max_pos >= max_seq)
+        return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const int nz = max_pos / QMH_WG + 1;
+    hipLaunchKernelGGL(k_bt_scores, dim3(n_heads, B, nz), dim3(QMH_WG), 0, s, Q, Kt, kv_stride, pos, att, n_heads,
+                       n_kv, hd, max_seq, scale);
+    hipLaunchKernelGGL(k_bt_softmax, dim3(n_heads, B), dim3(QMH_WG), 0, s, att, pos, n_heads, max_seq);
+    hipLaunchKernelGGL(k_bt_pv, dim3(n_heads, B), dim3(BT_PV), 0, s, att, V, kv_stride, pos, out, n_heads, n_kv, hd,
+                       max_seq);
+    return (int)hipGetLastError();
+}
+
+namespace {
+
+// first index of the maximum of row blockIdx.x (src/sampler.c:27-32), then the sequence's next
+// token and position for the device greedy loop; record[step*B + b] = idx when record != NULL
+__global__ __launch_bounds__(1024) void k_bt_argmax(const float *__restrict__ logits, int V, int32_t *tok,
+                                                    int32_t *pos, int32_t *record, int step) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int b = blockIdx.x, B = gridDim.x;
+    const float *x = logits + (size_t)b * V;
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+        const float xv = x[i];
+        if (xv == xv && (idx == 0x7fffffff || xv > v)) {
+            v = xv;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(idx, o);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[w] = v;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x >> 6); k++)
+            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
+                v = bv[k];
+                idx = bi[k];
+            }
+        if (idx == 0x7fffffff || x[0] != x[0]) idx = 0;  // all NaN, or NaN at 0
+        tok[b] = idx;
+        pos[b] += 1;
+        if (record) record[(size_t)step * B + b] = idx;
+    }
+}
+
+}  // namespace
+
+extern "C" int qmh_launch_bt_argmax(const float *logits, int B, int V, int32_t *tok, int32_t *pos, int32_t *record,
+                                    int step, void *stream) {
+    hipLaunchKernelGGL(k_bt_argmax, dim3(B), dim3(1024), 0, (hipStream_t)stream, logits, V, tok, pos, record, step);
+    return (int)hipGetLastError();
+}

@@ -99,6 +99,10 @@ typedef struct {
     int ld0, seg1, seg2;
     const float *rope;
     int pos0, head_dim, max_seq, kvd;
+    /* QKV of independent sequences (batched decode): token p is at position pos_arr[p] and writes the
+     * caches at out1/out2 + p*kv_stride; NULL / 0 for one prompt at positions pos0 + p */
+    const int32_t *pos_arr;
+    long long kv_stride;
 } qmh_pf_args;
 int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tokens, int P, float *X,
                         void *stream);
@@ -109,6 +113,18 @@ int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream);
 /* causal attention of P tokens at positions pos0.. over the caches; att: scratch [n_heads][P][max_seq] */
 int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P, int pos0,
                             int n_heads, int n_kv, int hd, int max_seq, float scale, void *stream);
+
+/* attention of B independent sequences, one query each (src/model.c:127-156 per sequence): sequence b
+ * at position pos[b] (device), query Q[b][n_heads*hd], caches Kt + b*kv_stride ([kvd][max_seq]) and
+ * V + b*kv_stride ([max_seq][kvd]); att: scratch [B][n_heads][max_seq]; out[b][n_heads*hd].
+ * max_pos: the largest pos[b] (sizes the grid). */
+int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride, const int32_t *pos,
+                            int max_pos, float *att, float *out, int B, int n_heads, int n_kv, int hd, int max_seq,
+                            float scale, void *stream);
+
+/* per row b of logits[B][V]: tok[b] = first argmax, pos[b] += 1, record[step*B + b] = it (if record) */
+int qmh_launch_bt_argmax(const float *logits, int B, int V, int32_t *tok, int32_t *pos, int32_t *record, int step,
+                         void *stream);
 
 /* argmax over x[n] -> *out_idx; if tokpos != NULL also tokpos[0] = idx, tokpos[1] += 1 and
  * record[step] = idx (when step < record_cap) where step = tokpos[2]++ (device greedy loop state) */

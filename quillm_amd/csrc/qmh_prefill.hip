@@ -283,7 +283,8 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
                     const float up = s[NM - 1][r][tt][e];
                     a.out0[(size_t)p * a.ld0 + row] = y / (1.0f + qmh_expf(-y)) * up;
                 } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
-                    const int pos = a.pos0 + p;
+                    const int pos = a.pos_arr ? a.pos_arr[p] : a.pos0 + p;
+                    float *kc = a.out1 + (size_t)p * a.kv_stride, *vc = a.out2 + (size_t)p * a.kv_stride;
                     if (row < a.seg2) {
                         const int local = row < a.seg1 ? row : row - a.seg1;
                         const float *cs =
@@ -292,9 +293,9 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
                         const float partner = s[0][r][tt][e ^ 1];  // rows 2i, 2i+1 share the lane
                         const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
                         if (row < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
-                        else a.out1[(size_t)local * a.max_seq + pos] = v;
+                        else kc[(size_t)local * a.max_seq + pos] = v;
                     } else {
-                        a.out2[(size_t)pos * a.kvd + (row - a.seg2)] = y;
+                        vc[(size_t)pos * a.kvd + (row - a.seg2)] = y;
                     }
                 }
             }
@@ -304,13 +305,25 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
 // token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
 // more leave too few waves to cover the latency at P = 512.
-enum { PF_NR = 2, PF_TW = 4, PF_PD = 2 };
+enum { PF_NR = 2, PF_TW = 4, PF_PD = 2, PF_PD_SMALL = 8 };
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
+    if (a->P <= 16) {  // decode-sized batches: one 16-row x 16-token tile per wave, twice the waves,
+                       // deeper prefetch (the stream is latency-bound, not MFMA-bound)
+        const dim3 g(1, (a->rows + 63) / 64);
+        if (a->il) {
+            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 2, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
+            else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 2, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
+        } else {
+            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 1, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
+            else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 1, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
+        }
+        return (int)hipGetLastError();
+    }
     // token groups past P are not launched; 16 * PF_TW divides PP, so every B load stays in the
     // PP-token activation buffer
     const dim3 g((a->P + 16 * PF_TW - 1) / (16 * PF_TW), (a->rows + 64 * PF_NR - 1) / (64 * PF_NR));

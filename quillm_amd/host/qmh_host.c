@@ -847,12 +847,26 @@ static void pf_args_for(const qmh_model *m, const struct qmh_weight *w, int P, q
     a->P = P;
 }
 
-/* one layer for P tokens at positions pos.. (src/model.c:164-187, token by token in the reference) */
-static int pf_layer(qmh_model *m, int l, int P, int pos, hipStream_t s) {
+/* independent sequences of a batched decode step: token p at position pos[p] (device), its caches
+ * at kt/v + p*kv_stride; max_pos is the largest position */
+typedef struct {
+    const int32_t *pos;
+    int max_pos;
+    float *kt, *v;
+    long long kv_stride;
+} pf_seqs;
+
+/* one layer for P tokens (src/model.c:164-187, token by token in the reference): a prompt at positions
+ * pos.. in the model's caches, or (bt != NULL) one token of each of P independent sequences */
+static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipStream_t s) {
     const qmh_config *c = &m->cfg;
     const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq, PP = m->pf_pp;
     dev_layer *L = &m->layers[l];
     float *kl = m->d_kt + (size_t)l * S_ * m->kvd, *vl = m->d_v + (size_t)l * S_ * m->kvd;
+    if (bt) {
+        kl = bt->kt + (size_t)l * P * bt->kv_stride;
+        vl = bt->v + (size_t)l * P * bt->kv_stride;
+    }
     qmh_pf_args a;
     /* q, k, v = W rmsnorm(x); rope; k, v -> caches */
     LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * l) * D, c->norm_eps, D, P, m->d_pf_xc, m->d_pf_xd,
@@ -871,9 +885,17 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, hipStream_t s) {
     a.head_dim = m->hd;
     a.max_seq = S_;
     a.kvd = m->kvd;
+    if (bt) {
+        a.pos_arr = bt->pos;
+        a.kv_stride = bt->kv_stride;
+    }
     LCHK(qmh_launch_pf_gemm(&a, s));
-    LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads, m->hd,
-                                 S_, 1.0f / sqrtf((float)m->hd), s));
+    if (bt)
+        LCHK(qmh_launch_bt_attention(m->d_pf_q, kl, vl, bt->kv_stride, bt->pos, bt->max_pos, m->d_pf_att, m->d_pf_xb,
+                                     P, c->n_heads, c->n_kv_heads, m->hd, S_, 1.0f / sqrtf((float)m->hd), s));
+    else
+        LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads,
+                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), s));
     /* x += Wo xb */
     LCHK(qmh_launch_pf_quant(m->d_pf_xb, D, NULL, 0.0f, D, P, m->d_pf_xc, m->d_pf_xd, PP, L->wo.dtype == QMH_Q4_0, s));
     pf_args_for(m, &L->wo, P, &a);
@@ -913,7 +935,7 @@ static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
         HIPCHK(hipMemcpyAsync(m->d_pf_tok, m->h_pf_tok, sizeof(int32_t) * (size_t)P, hipMemcpyHostToDevice, g_stream));
         LCHK(qmh_launch_pf_embed(m->d_embd, m->emb_dtype, D, V, m->d_pf_tok, P, m->d_pf_x, g_stream));
         for (int l = 0; l < c->n_layers; l++)
-            if (pf_layer(m, l, P, pos, g_stream)) return -1;
+            if (pf_layer(m, l, P, pos, NULL, g_stream)) return -1;
         if (logits) { /* logits = Woutput rmsnorm(x) for every position (src/model.c:188-189) */
             qmh_pf_args a;
             LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * c->n_layers) * D, c->norm_eps, D, P,
@@ -960,6 +982,159 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
     for (int32_t k = 0; k < n_steps; k++) HIPCHK(run_step(m, 1));
     if (n_steps > 0 && out)
         HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+/* ------------------------------------------------------------------ batched decode */
+
+/* B independent sequences over one model's weights: each has its own KV cache (layout per layer
+ * [seq][kvd][max_seq] for K, [seq][max_seq][kvd] for V); a step runs the B tokens through the
+ * prefill kernels as one batch, with attention per sequence. */
+struct qmh_batch {
+    qmh_model *m;
+    int32_t n;
+    float *d_kt, *d_v;
+    int32_t *d_tok, *d_pos, *d_record;
+    int32_t *h_io; /* pinned [2n]: tokens, positions */
+    int record_cap;
+};
+
+void qmh_batch_free(qmh_batch *b) {
+    if (!b) return;
+    void *bufs[] = {b->d_kt, b->d_v, b->d_tok, b->d_pos, b->d_record};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
+        if (bufs[i]) hipFree(bufs[i]);
+    if (b->h_io) hipHostFree(b->h_io);
+    free(b);
+}
+
+qmh_batch *qmh_batch_create(qmh_model *m, int32_t n_seq) {
+    if (!m) {
+        fail("batch: NULL model");
+        return NULL;
+    }
+    if (!m->pf_ok) {
+        fail("batch: needs quantized weights and head_dim <= 128 (the batched matmul path)");
+        return NULL;
+    }
+    if (n_seq < 1 || n_seq > m->pf_cap || m->hd > 128) {
+        fail("batch: n_seq %d outside [1, %d] or head_dim %d > 128", (int)n_seq, m->pf_cap, m->hd);
+        return NULL;
+    }
+    qmh_batch *b = calloc(1, sizeof *b);
+    if (!b) {
+        fail("batch: out of host memory");
+        return NULL;
+    }
+    const qmh_config *c = &m->cfg;
+    const size_t kv = (size_t)c->n_layers * n_seq * m->kvd * c->max_seq;
+    b->m = m;
+    b->n = n_seq;
+    b->record_cap = c->max_seq;
+    hipError_t e = hipMalloc((void **)&b->d_kt, kv * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&b->d_v, kv * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&b->d_tok, sizeof(int32_t) * (size_t)n_seq);
+    if (e == hipSuccess) e = hipMalloc((void **)&b->d_pos, sizeof(int32_t) * (size_t)n_seq);
+    if (e == hipSuccess) e = hipMalloc((void **)&b->d_record, sizeof(int32_t) * (size_t)n_seq * c->max_seq);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&b->h_io, sizeof(int32_t) * 2 * (size_t)n_seq, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMemsetAsync(b->d_kt, 0, kv * sizeof(float), g_stream);
+    if (e == hipSuccess) e = hipMemsetAsync(b->d_v, 0, kv * sizeof(float), g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        fail("batch: %s", hipGetErrorString(e));
+        qmh_batch_free(b);
+        return NULL;
+    }
+    return b;
+}
+
+static int batch_check(const qmh_batch *b, const int32_t *tokens, const int32_t *pos, int32_t steps, int *max_pos) {
+    const qmh_config *c = &b->m->cfg;
+    *max_pos = 0;
+    for (int32_t i = 0; i < b->n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= c->vocab_size) return fail("batch: sequence %d token %d out of range", i, tokens[i]);
+        if (pos[i] < 0 || (int64_t)pos[i] + steps > c->max_seq)
+            return fail("batch: sequence %d position %d (+%d steps) outside [0, %d)", i, pos[i], steps, c->max_seq);
+        if (pos[i] > *max_pos) *max_pos = pos[i];
+    }
+    return 0;
+}
+
+/* one step: embed, the layers, and the logits of all sequences into d_pf_logits */
+static int batch_step(qmh_batch *b, int max_pos, hipStream_t s) {
+    qmh_model *m = b->m;
+    const qmh_config *c = &m->cfg;
+    const int D = c->dim, V = c->vocab_size, B = b->n;
+    pf_seqs bt = {b->d_pos, max_pos, b->d_kt, b->d_v, (long long)m->kvd * c->max_seq};
+    LCHK(qmh_launch_pf_embed(m->d_embd, m->emb_dtype, D, V, b->d_tok, B, m->d_pf_x, s));
+    for (int l = 0; l < c->n_layers; l++)
+        if (pf_layer(m, l, B, 0, &bt, s)) return -1;
+    qmh_pf_args a;
+    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * c->n_layers) * D, c->norm_eps, D, B, m->d_pf_xc,
+                             m->d_pf_xd, m->pf_pp, m->output.dtype == QMH_Q4_0, s));
+    pf_args_for(m, &m->output, B, &a);
+    a.rows_alloc = m->output.ntiles * m->output.tile_r;
+    a.epi = QMH_PF_STORE;
+    a.out0 = m->d_pf_logits;
+    a.ld0 = V;
+    LCHK(qmh_launch_pf_gemm(&a, s));
+    return 0;
+}
+
+int qmh_batch_forward(qmh_batch *b, const int32_t *tokens, const int32_t *pos, float *logits) {
+    if (!b || !tokens || !pos) return fail("batch_forward: NULL argument");
+    int max_pos;
+    if (batch_check(b, tokens, pos, 1, &max_pos)) return -1;
+    const int B = b->n, V = b->m->cfg.vocab_size;
+    memcpy(b->h_io, tokens, sizeof(int32_t) * (size_t)B);
+    memcpy(b->h_io + B, pos, sizeof(int32_t) * (size_t)B);
+    HIPCHK(hipMemcpyAsync(b->d_tok, b->h_io, sizeof(int32_t) * (size_t)B, hipMemcpyHostToDevice, g_stream));
+    HIPCHK(hipMemcpyAsync(b->d_pos, b->h_io + B, sizeof(int32_t) * (size_t)B, hipMemcpyHostToDevice, g_stream));
+    if (batch_step(b, max_pos, g_stream)) return -1;
+    if (logits)
+        HIPCHK(hipMemcpyAsync(logits, b->m->d_pf_logits, sizeof(float) * (size_t)B * V, hipMemcpyDeviceToHost,
+                              g_stream));
+    HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int qmh_batch_greedy(qmh_batch *b, const int32_t *tokens, const int32_t *pos, int32_t n_steps, int32_t *out,
+                     double *ms) {
+    if (!b || !tokens || !pos || n_steps < 0) return fail("batch_greedy: bad argument");
+    int max_pos;
+    if (batch_check(b, tokens, pos, n_steps, &max_pos)) return -1;
+    const int B = b->n, V = b->m->cfg.vocab_size;
+    memcpy(b->h_io, tokens, sizeof(int32_t) * (size_t)B);
+    memcpy(b->h_io + B, pos, sizeof(int32_t) * (size_t)B);
+    HIPCHK(hipMemcpyAsync(b->d_tok, b->h_io, sizeof(int32_t) * (size_t)B, hipMemcpyHostToDevice, g_stream));
+    HIPCHK(hipMemcpyAsync(b->d_pos, b->h_io + B, sizeof(int32_t) * (size_t)B, hipMemcpyHostToDevice, g_stream));
+    hipEvent_t e0 = NULL, e1 = NULL;
+    if (ms) {
+        HIPCHK(hipEventCreate(&e0));
+        HIPCHK(hipEventCreate(&e1));
+        HIPCHK(hipEventRecord(e0, g_stream));
+    }
+    int rc = 0;
+    for (int32_t k = 0; k < n_steps && !rc; k++) {
+        rc = batch_step(b, max_pos + k, g_stream);
+        if (!rc) rc = qmh_launch_bt_argmax(b->m->d_pf_logits, B, V, b->d_tok, b->d_pos, b->d_record, k, g_stream)
+                          ? fail("batch_greedy: argmax launch failed")
+                          : 0;
+    }
+    if (!rc && ms) {
+        HIPCHK(hipEventRecord(e1, g_stream));
+        HIPCHK(hipEventSynchronize(e1));
+        float f = 0.0f;
+        HIPCHK(hipEventElapsedTime(&f, e0, e1));
+        *ms = f;
+    }
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (rc) return -1;
+    if (n_steps > 0 && out)
+        HIPCHK(hipMemcpyAsync(out, b->d_record, sizeof(int32_t) * (size_t)n_steps * B, hipMemcpyDeviceToHost,
+                              g_stream));
     HIPCHK(hipStreamSynchronize(g_stream));
     return 0;
 }
