@@ -28,12 +28,12 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_scores(const float *__restrict__ 
     if (t > pos) return;
     const float *kc = Kt + (size_t)b * kv_stride + (size_t)kvh * hd * max_seq + t;
     float s = 0.0f;
-    for (int d0 = 0; d0 < hd; d0 += 8) {
-        float kv[8];
+    for (int d0 = 0; d0 < hd; d0 += 64) {  // 64 loads in flight
+        float kv[64];
 #pragma unroll
-        for (int j = 0; j < 8; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
+        for (int j = 0; j < 64; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < 64; j++)
             if (d0 + j < hd) s = s + qs[d0 + j] * kv[j];
     }
     att[((size_t)b * n_heads + h) * max_seq + t] = s * scale;
@@ -71,33 +71,49 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_softmax(float *att, const int32_t
     for (int t = threadIdx.x; t < n; t += QMH_WG) x[t] = x[t] * inv;
 }
 
-// out[b][h*hd + i] = +0 + p_0 v_0[i] + ... + p_pos v_pos[i]: thread i runs column i's chain; the
-// probabilities pass through LDS 256 positions at a time, V rows are read 8 positions ahead
-constexpr int BT_PV = 128;
-__global__ __launch_bounds__(BT_PV) void k_bt_pv(const float *__restrict__ att, const float *__restrict__ V,
-                                                 long long kv_stride, const int32_t *__restrict__ pos_arr,
-                                                 float *out, int n_heads, int n_kv, int hd, int max_seq) {
-    __shared__ float ps[256];
-    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x, n = pos_arr[b] + 1;
-    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv;
+// out[b][h*hd + i] = +0 + p_0 v_0[i] + ... + p_pos v_pos[i]: thread i < hd runs column i's chain.
+// V passes through LDS 64 positions at a time (cooperative float4 loads; the next chunk is held in
+// registers while the current one is used), the probabilities with it.
+constexpr int BT_VC = 64;
+__global__ __launch_bounds__(QMH_WG) void k_bt_pv(const float *__restrict__ att, const float *__restrict__ V,
+                                                  long long kv_stride, const int32_t *__restrict__ pos_arr,
+                                                  float *out, int n_heads, int n_kv, int hd, int max_seq) {
+    __shared__ __align__(16) float vs[BT_VC * 128];  // [t][column]
+    __shared__ float ps[BT_VC];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, n = pos_arr[b] + 1;
+    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, hd4 = hd >> 2;
     const float *prow = att + ((size_t)b * n_heads + h) * max_seq;
-    const float *vcol = V + (size_t)b * kv_stride + (size_t)kvh * hd + (i < hd ? i : 0);
+    const float *vbase = V + (size_t)b * kv_stride + (size_t)kvh * hd;
+    constexpr int VR = BT_VC * 32 / QMH_WG;  // float4 slots per thread per chunk (32 per row)
+    float4 vr[VR];
+    float pr = 0.0f;
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * QMH_WG + tid, t = e >> 5, c4 = e & 31;
+            const int tc = c0 + t < n ? c0 + t : n - 1;
+            vr[k] = c4 < hd4 ? *(const float4 *)(vbase + (size_t)tc * kvd + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (tid < BT_VC) pr = c0 + tid < n ? prow[c0 + tid] : 0.0f;
+    };
     float acc = 0.0f;
-    for (int c0 = 0; c0 < n; c0 += 256) {
-        const int nt = min(256, n - c0);
+    load(0);
+    for (int c0 = 0; c0 < n; c0 += BT_VC) {
         __syncthreads();
-        for (int k = i; k < nt; k += BT_PV) ps[k] = prow[c0 + k];
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * QMH_WG + tid;
+            *(float4 *)(vs + (e >> 5) * 128 + 4 * (e & 31)) = vr[k];
+        }
+        if (tid < BT_VC) ps[tid] = pr;
+        if (c0 + BT_VC < n) load(c0 + BT_VC);
         __syncthreads();
-        for (int t0 = 0; t0 < nt; t0 += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = vcol[(size_t)(c0 + (t0 + j < nt ? t0 + j : nt - 1)) * kvd];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (t0 + j < nt) acc = acc + ps[t0 + j] * v[j];
+        if (tid < hd) {
+            const int nt = min(BT_VC, n - c0);
+            for (int t = 0; t < nt; t++) acc = acc + ps[t] * vs[t * 128 + tid];
         }
     }
-    if (i < hd) out[(size_t)b * n_heads * hd + h * hd + i] = acc;
+    if (tid < hd) out[(size_t)b * n_heads * hd + h * hd + tid] = acc;
 }
 
 }  // namespace
@@ -105,14 +121,14 @@ __global__ __launch_bounds__(BT_PV) void k_bt_pv(const float *__restrict__ att, 
 extern "C" int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride,
                                        const int32_t *pos, int max_pos, float *att, float *out, int B, int n_heads,
                                        int n_kv, int hd, int max_seq, float scale, void *stream) {
-    if (B < 1 || hd < 1 || hd > 128 || n_kv < 1 || n_heads % n_kv || max_pos < 0 || max_pos >= max_seq)
+    if (B < 1 || hd < 4 || hd > 128 || hd % 4 || n_kv < 1 || n_heads % n_kv || max_pos < 0 || max_pos >= max_seq)
         return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const int nz = max_pos / QMH_WG + 1;
     hipLaunchKernelGGL(k_bt_scores, dim3(n_heads, B, nz), dim3(QMH_WG), 0, s, Q, Kt, kv_stride, pos, att, n_heads,
                        n_kv, hd, max_seq, scale);
     hipLaunchKernelGGL(k_bt_softmax, dim3(n_heads, B), dim3(QMH_WG), 0, s, att, pos, n_heads, max_seq);
-    hipLaunchKernelGGL(k_bt_pv, dim3(n_heads, B), dim3(BT_PV), 0, s, att, V, kv_stride, pos, out, n_heads, n_kv, hd,
+    hipLaunchKernelGGL(k_bt_pv, dim3(n_heads, B), dim3(QMH_WG), 0, s, att, V, kv_stride, pos, out, n_heads, n_kv, hd,
                        max_seq);
     return (int)hipGetLastError();
 }

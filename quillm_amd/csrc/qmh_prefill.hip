@@ -63,59 +63,102 @@ extern "C" int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, 
 // token-major-within-block image: codes xc[(b*PP + p)*32 + k], scales xd[b*PP + p] (fp32 of the
 // fp16 d). perm8: codes of each 8-group in the order e0 e2 e4 e6 e1 e3 e5 e7 (Q4_0 consumers).
 // One workgroup per token; 8 lanes per block, 4 values each, as the decode prologue.
+// One thread's share of a block quantization: block b = 32*r + tid/8 (round r), values 4*(tid%8)
+// .. +3 of it, as the decode prologue (amax over 8 lanes by DPP), then the codes and the scale.
+__device__ __forceinline__ void pf_quant_block(const float (&v)[4], int b, int nb, int p, int sub, int8_t *xc,
+                                               float *xd, int PP, int perm8) {
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float av = fabsf(v[j]);
+        m = av > m ? av : m;
+    }
+    m = qmh_amax8(m);
+    const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
+    int q[4];
+    qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
+    if (b < nb) {
+        int8_t *c = xc + ((size_t)b * PP + p) * 32;
+        if (perm8) {  // elements 8g+e (e = 0..7) at 8g + {0,4,1,5,2,6,3,7}[e]
+            const int g = sub >> 1, e0 = (sub & 1) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = e0 + j;
+                c[8 * g + ((e & 1) ? 4 + (e >> 1) : (e >> 1))] = (int8_t)q[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) c[sub * 4 + j] = (int8_t)q[j];
+        }
+        if (sub == 0) xd[(size_t)b * PP + p] = dd;
+    }
+}
+
+// One workgroup per token; 8 lanes per block, 4 values each. Rows of up to PQ_R*1024 values are
+// loaded once into registers (one round of loads), larger ones round by round.
+#define PQ_R 16
 __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x, int ldx, const float *w, float eps,
                                                      int n, int8_t *xc, float *xd, int PP, int perm8) {
     __shared__ double red[16];
     const int p = blockIdx.x, tid = threadIdx.x, nb = (n + 31) / 32, sub = tid & 7;
+    const int R = (nb + QMH_WG / 8 - 1) / (QMH_WG / 8);  // rounds of 32 blocks
     const float *row = x + (size_t)p * ldx;
+    const bool held = R <= PQ_R;
+    float xv[PQ_R][4];
+    double ss = 0.0;
+    if (held) {
+#pragma unroll
+        for (int r = 0; r < PQ_R; r++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = (r * (QMH_WG / 8) + (tid >> 3)) * 32 + sub * 4 + j;
+                xv[r][j] = (r < R && i < n) ? row[i] : 0.0f;
+            }
+        if (w)
+#pragma unroll
+            for (int r = 0; r < PQ_R; r++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) ss += (double)xv[r][j] * (double)xv[r][j];
+    } else if (w) {
+        for (int i = tid; i < n; i += QMH_WG) ss += (double)row[i] * (double)row[i];
+    }
     float inv = 1.0f;
     if (w) {
-        double ss = 0.0;
-        for (int i = tid; i < n; i += QMH_WG) ss += (double)row[i] * (double)row[i];
         ss = qmh_block_sum_d(ss, red);
         const double d = qmh_sum_slack(ss, n);
         inv = qmh_rms_inv(ss - d, n, eps);
         if (inv != qmh_rms_inv(ss + d, n, eps)) {  // uniform; serial sum as the reference
             if (tid == 0) {
-                double s = 0.0;
-                for (int i = 0; i < n; i++) s += (double)row[i] * (double)row[i];
-                red[8] = s;
+                double s2 = 0.0;
+                for (int i = 0; i < n; i++) s2 += (double)row[i] * (double)row[i];
+                red[8] = s2;
             }
             __syncthreads();
             inv = qmh_rms_inv(red[8], n, eps);
         }
     }
-    for (int b0 = 0; b0 < nb; b0 += QMH_WG / 8) {  // uniform trip count: DPP needs all 8 lanes
-        const int b = b0 + (tid >> 3), i4 = b * 32 + sub * 4;
-        const bool on = b < nb;
-        float v[4], m = 0.0f;
+    // (x*inv)*w as the reference; rounds are uniform (DPP needs all 8 lanes of a block)
+    if (held) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = i4 + j;
-            float xv = (on && i < n) ? row[i] : 0.0f;
-            if (w) xv = (on && i < n) ? xv * inv * w[i] : 0.0f;  // (x*inv)*w as the reference
-            v[j] = xv;
-            const float av = fabsf(xv);
-            m = av > m ? av : m;
-        }
-        m = qmh_amax8(m);
-        const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
-        int q[4];
-        qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
-        if (on) {
-            int8_t *c = xc + ((size_t)b * PP + p) * 32;
-            if (perm8) {  // elements 8g+e (e = 0..7) at 8g + {0,4,1,5,2,6,3,7}[e]
-                const int g = sub >> 1, e0 = (sub & 1) * 4;
+        for (int r = 0; r < PQ_R; r++)
+            if (r < R) {
+                const int b = r * (QMH_WG / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
+                float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int e = e0 + j;
-                    c[8 * g + ((e & 1) ? 4 + (e >> 1) : (e >> 1))] = (int8_t)q[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; j++) c[sub * 4 + j] = (int8_t)q[j];
+                for (int j = 0; j < 4; j++)
+                    v[j] = w ? ((b < nb && i4 + j < n) ? xv[r][j] * inv * w[i4 + j] : 0.0f) : xv[r][j];
+                pf_quant_block(v, b, nb, p, sub, xc, xd, PP, perm8);
             }
-            if (sub == 0) xd[(size_t)b * PP + p] = dd;
+    } else {
+        for (int r = 0; r < R; r++) {
+            const int b = r * (QMH_WG / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool in = b < nb && i4 + j < n;
+                v[j] = in ? (w ? row[i4 + j] * inv * w[i4 + j] : row[i4 + j]) : 0.0f;
+            }
+            pf_quant_block(v, b, nb, p, sub, xc, xd, PP, perm8);
         }
     }
 }
@@ -216,6 +259,31 @@ __device__ __forceinline__ void pf_mul(const PfBlock<NM, NR, TW> &cur, float (&s
         }
 }
 
+// one output of the matmul: y = row's value for token p (up: the W3 value of the SwiGLU pair;
+// partner: the value of row ^ 1, RoPE's pair), stored as the epilogue asks
+__device__ __forceinline__ void pf_store(const qmh_pf_args &a, int row, int p, float y, float up, float partner) {
+    if (a.epi == QMH_PF_STORE) {
+        a.out0[(size_t)p * a.ld0 + row] = y;
+    } else if (a.epi == QMH_PF_ADD) {  // x += W x' (src/model.c:179,186)
+        a.out0[(size_t)p * a.ld0 + row] = a.out0[(size_t)p * a.ld0 + row] + y;
+    } else if (a.epi == QMH_PF_SWIGLU) {  // silu(g)*u (src/ops.c:128-133)
+        a.out0[(size_t)p * a.ld0 + row] = y / (1.0f + qmh_expf(-y)) * up;
+    } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
+        const int pos = a.pos_arr ? a.pos_arr[p] : a.pos0 + p;
+        float *kc = a.out1 + (size_t)p * a.kv_stride, *vc = a.out2 + (size_t)p * a.kv_stride;
+        if (row < a.seg2) {
+            const int local = row < a.seg1 ? row : row - a.seg1;
+            const float *cs = a.rope + ((size_t)pos * (a.head_dim >> 1) + ((local % a.head_dim) >> 1)) * 2;
+            const float c = cs[0], sn = cs[1];
+            const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
+            if (row < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
+            else kc[(size_t)local * a.max_seq + pos] = v;
+        } else {
+            vc[(size_t)pos * a.kvd + (row - a.seg2)] = y;
+        }
+    }
+}
+
 template <int WT, int NM, int NR, int TW, int PD>
 __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4;
@@ -274,44 +342,106 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
             for (int e = 0; e < 4; e++) {
                 const int row = r0 + 16 * r + 4 * kq + e;
                 if (row >= a.rows) continue;
-                const float y = s[0][r][tt][e];
-                if (a.epi == QMH_PF_STORE) {
-                    a.out0[(size_t)p * a.ld0 + row] = y;
-                } else if (a.epi == QMH_PF_ADD) {  // x += W x' (src/model.c:179,186)
-                    a.out0[(size_t)p * a.ld0 + row] = a.out0[(size_t)p * a.ld0 + row] + y;
-                } else if (a.epi == QMH_PF_SWIGLU) {  // silu(g)*u (src/ops.c:128-133)
-                    const float up = s[NM - 1][r][tt][e];
-                    a.out0[(size_t)p * a.ld0 + row] = y / (1.0f + qmh_expf(-y)) * up;
-                } else {  // QKV: rope on q and k (src/ops.c:114-126), k/v into the caches
-                    const int pos = a.pos_arr ? a.pos_arr[p] : a.pos0 + p;
-                    float *kc = a.out1 + (size_t)p * a.kv_stride, *vc = a.out2 + (size_t)p * a.kv_stride;
-                    if (row < a.seg2) {
-                        const int local = row < a.seg1 ? row : row - a.seg1;
-                        const float *cs =
-                            a.rope + ((size_t)pos * (a.head_dim >> 1) + ((local % a.head_dim) >> 1)) * 2;
-                        const float c = cs[0], sn = cs[1];
-                        const float partner = s[0][r][tt][e ^ 1];  // rows 2i, 2i+1 share the lane
-                        const float v = (local & 1) == 0 ? (y * c - partner * sn) : (partner * sn + y * c);
-                        if (row < a.seg1) a.out0[(size_t)p * a.ld0 + local] = v;
-                        else kc[(size_t)local * a.max_seq + pos] = v;
-                    } else {
-                        vc[(size_t)pos * a.kvd + (row - a.seg2)] = y;
-                    }
-                }
+                // rows 2i, 2i+1 share the lane (RoPE partner)
+                pf_store(a, row, p, s[0][r][tt][e], s[NM - 1][r][tt][e], s[0][r][tt][e ^ 1]);
             }
         }
+}
+
+// Skinny matmul for decode-sized batches (P <= 16 tokens): one workgroup per 16-row group, its 8
+// waves splitting the blocks (wave w: blocks w, w+8, ...), PD at a time in flight. Each block's
+// exact int32 dot comes from one MFMA with a zero accumulator, and its term (float)acc*(dw*dx)
+// goes to LDS at [matrix][block][row][token]; then one thread per (row, token) runs the serial
+// chain over the blocks in order (the reference's order) and the epilogue. Dynamic LDS:
+// NM*nb*16*P floats.
+#define SK_WG 512
+template <int WT, int NM, int PD>
+__global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
+    extern __shared__ float T[];
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4, tok = l & 15;
+    const int r0 = blockIdx.x * 16, P = a.P, nb = a.nb;
+    constexpr int CB = WT == QMH_Q8 ? 32 : 16;
+    PfLane<NM, 1> ln;
+    {
+        const int row = r0 + tok, grp = r0 + 4 * kq;  // A row; first D row
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            ln.a[m][0] = pf_slot0(a, row < a.rows_alloc ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
+            ln.s[m][0] = pf_slot0(a, grp < a.rows_alloc ? grp : 0, m);
+        }
+    }
+    ln.x = (uint32_t)tok * 32 + 8 * kq;
+    ln.d = (uint32_t)tok;
+    for (int b0 = wave; b0 < nb; b0 += 8 * PD) {
+        PfBlock<NM, 1, 1> blk[PD];
+#pragma unroll
+        for (int j = 0; j < PD; j++) {
+            const int b = b0 + 8 * j;
+            pf_load<WT, NM, 1, 1>(a, b < nb ? b : nb - 1, ln, blk[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < PD; j++) {
+            const int b = b0 + 8 * j;
+            if (b >= nb) break;
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const uint2 sc = blk[j].sc[m][0];
+                const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
+                                     qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
+                const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
+                const pf_v4i z = {0, 0, 0, 0};
+                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[0], z, 0, 0, 0);
+                if (tok < P)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        T[(((size_t)m * nb + b) * 16 + 4 * kq + e) * P + tok] = (float)acc[e] * (dw[e] * blk[j].dx[0]);
+            }
+        }
+    }
+    __syncthreads();
+    // chains: thread c = token*16 + row, for c < 16*P
+    const int c = threadIdx.x, row = c & 15, p = c >> 4;
+    const bool on = p < P;
+    float y[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        float s = 0.0f;
+        if (on)
+            for (int b = 0; b < nb; b++) s = s + T[(((size_t)m * nb + b) * 16 + row) * P + p];
+        y[m] = s;
+    }
+    const float partner = __shfl_xor(y[0], 1);  // row ^ 1 of the same token: RoPE's pair
+    if (on && r0 + row < a.rows) pf_store(a, r0 + row, p, y[0], y[NM - 1], partner);
+}
+
+// LDS a skinny matmul needs, or 0 when it does not fit (then the tiled instance runs)
+static size_t sk_lds(const qmh_pf_args *a) {
+    const size_t b = (size_t)(a->il ? 2 : 1) * a->nb * 16 * a->P * sizeof(float);
+    return b <= 160 * 1024 ? b : 0;
 }
 
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
 // token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
 // more leave too few waves to cover the latency at P = 512.
-enum { PF_NR = 2, PF_TW = 4, PF_PD = 2, PF_PD_SMALL = 8 };
+enum { PF_NR = 2, PF_TW = 4, PF_PD = 2, PF_PD_SMALL = 8, SK_PD = 8 };
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
+    if (a->P <= 16 && sk_lds(a)) {  // decode-sized batches whose terms fit LDS
+        const dim3 g((a->rows + 15) / 16);
+        const size_t lds = sk_lds(a);
+        if (a->il) {
+            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_sk_gemm<QMH_Q4, 2, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+            else hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, 2, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+        } else {
+            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_sk_gemm<QMH_Q4, 1, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+            else hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, 1, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+        }
+        return (int)hipGetLastError();
+    }
     if (a->P <= 16) {  // decode-sized batches: one 16-row x 16-token tile per wave, twice the waves,
                        // deeper prefetch (the stream is latency-bound, not MFMA-bound)
         const dim3 g(1, (a->rows + 63) / 64);
