@@ -348,18 +348,30 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
         }
 }
 
-// Skinny matmul for decode-sized batches (P <= 16 tokens): one workgroup per 16-row group, its 8
-// waves splitting the blocks (wave w: blocks w, w+8, ...), PD at a time in flight. Each block's
-// exact int32 dot comes from one MFMA with a zero accumulator, and its term (float)acc*(dw*dx)
-// goes to LDS at [matrix][block][row][token]; then one thread per (row, token) runs the serial
-// chain over the blocks in order (the reference's order) and the epilogue. Dynamic LDS:
-// NM*nb*16*P floats.
+// Skinny matmul for decode-sized batches (P <= 16*TT tokens): one workgroup per 16-row group
+// streams every block of its rows once for all tokens. The blocks pass in rounds of as many as
+// fit the LDS budget at this P: wave w takes blocks base + 8j + w in batches of PD (each batch's
+// loads all in flight, no barrier inside a round), takes each block's exact int32 dot for TT
+// token tiles from MFMAs with a zero accumulator, and stores the term (float)acc*(dw*dx) in LDS
+// at [matrix][block in round][row][token]; after the round one thread per (row, token) pair
+// extends that pair's serial chain over the round's blocks in order (the reference's order).
+// After the last round each pair runs the epilogue. Dynamic LDS: one round's terms, at most SK_LDS.
 #define SK_WG 512
-template <int WT, int NM, int PD>
+#define SK_LDS (128 * 1024)
+// blocks per round: a multiple of 8 that fits the LDS budget at P tokens (the launch gives the
+// kernel exactly NM*16*P*4 bytes per block of a round)
+__host__ __device__ inline int sk_round(int nb, int nm, int P) {
+    const int fit = (SK_LDS / (nm * 16 * P * 4)) & ~7, all = (nb + 7) & ~7;
+    return fit < all ? fit : all;
+}
+template <int WT, int NM, int TT, int PD>
 __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
+    constexpr int PT = 16 * TT;
+    constexpr int NPAIR = 16 * PT / SK_WG > 0 ? 16 * PT / SK_WG : 1;  // (row, token) pairs per thread
     extern __shared__ float T[];
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4, tok = l & 15;
     const int r0 = blockIdx.x * 16, P = a.P, nb = a.nb;
+    const int rblk = sk_round(nb, NM, P);
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;
     PfLane<NM, 1> ln;
     {
@@ -372,86 +384,92 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
     }
     ln.x = (uint32_t)tok * 32 + 8 * kq;
     ln.d = (uint32_t)tok;
-    for (int b0 = wave; b0 < nb; b0 += 8 * PD) {
-        PfBlock<NM, 1, 1> blk[PD];
+    float s[NPAIR][NM];
 #pragma unroll
-        for (int j = 0; j < PD; j++) {
-            const int b = b0 + 8 * j;
-            pf_load<WT, NM, 1, 1>(a, b < nb ? b : nb - 1, ln, blk[j]);
-        }
+    for (int k = 0; k < NPAIR; k++)
 #pragma unroll
-        for (int j = 0; j < PD; j++) {
-            const int b = b0 + 8 * j;
-            if (b >= nb) break;
+        for (int m = 0; m < NM; m++) s[k][m] = 0.0f;
+    for (int base = 0; base < nb; base += rblk) {
+        const int nr = min(rblk, nb - base);
+        for (int k0 = 0; 8 * k0 + wave < nr; k0 += PD) {  // uniform per wave
+            PfBlock<NM, 1, TT> blk[PD];
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
-                const uint2 sc = blk[j].sc[m][0];
-                const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
-                                     qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
-                const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
-                const pf_v4i z = {0, 0, 0, 0};
-                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[0], z, 0, 0, 0);
-                if (tok < P)
+            for (int j = 0; j < PD; j++) {
+                const int jb = 8 * (k0 + j) + wave;
+                pf_load<WT, NM, 1, TT>(a, base + (jb < nr ? jb : nr - 1), ln, blk[j]);
+            }
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        T[(((size_t)m * nb + b) * 16 + 4 * kq + e) * P + tok] = (float)acc[e] * (dw[e] * blk[j].dx[0]);
+            for (int j = 0; j < PD; j++) {
+                const int jb = 8 * (k0 + j) + wave;
+                if (jb < nr)  // uniform per wave
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    const uint2 sc = blk[j].sc[m][0];
+                    const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
+                                         qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
+                    const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
+#pragma unroll
+                    for (int tt = 0; tt < TT; tt++) {
+                        const pf_v4i z = {0, 0, 0, 0};
+                        const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[tt], z, 0, 0, 0);
+                        const int p = 16 * tt + tok;
+                        if (p < P)
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                T[(((size_t)m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
+                                    (float)acc[e] * (dw[e] * blk[j].dx[tt]);
+                    }
+                }
             }
         }
-    }
-    __syncthreads();
-    // chains: thread c = token*16 + row, for c < 16*P
-    const int c = threadIdx.x, row = c & 15, p = c >> 4;
-    const bool on = p < P;
-    float y[NM];
+        __syncthreads();
 #pragma unroll
-    for (int m = 0; m < NM; m++) {
-        float s = 0.0f;
-        if (on)
-            for (int b = 0; b < nb; b++) s = s + T[(((size_t)m * nb + b) * 16 + row) * P + p];
-        y[m] = s;
+        for (int k = 0; k < NPAIR; k++) {
+            const int c = threadIdx.x + k * SK_WG, row = c & 15, p = c >> 4;
+            if (p < P)
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+                    for (int jb = 0; jb < nr; jb++) s[k][m] = s[k][m] + T[(((size_t)m * rblk + jb) * 16 + row) * P + p];
+        }
+        __syncthreads();
     }
-    const float partner = __shfl_xor(y[0], 1);  // row ^ 1 of the same token: RoPE's pair
-    if (on && r0 + row < a.rows) pf_store(a, r0 + row, p, y[0], y[NM - 1], partner);
-}
-
-// LDS a skinny matmul needs, or 0 when it does not fit (then the tiled instance runs)
-static size_t sk_lds(const qmh_pf_args *a) {
-    const size_t b = (size_t)(a->il ? 2 : 1) * a->nb * 16 * a->P * sizeof(float);
-    return b <= 160 * 1024 ? b : 0;
+#pragma unroll
+    for (int k = 0; k < NPAIR; k++) {
+        const int c = threadIdx.x + k * SK_WG, row = c & 15, p = c >> 4;
+        const float partner = __shfl_xor(s[k][0], 1);  // row ^ 1 of the same token: RoPE's pair
+        if (p < P && r0 + row < a.rows) pf_store(a, r0 + row, p, s[k][0], s[k][NM - 1], partner);
+    }
 }
 
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
 // token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
 // more leave too few waves to cover the latency at P = 512.
-enum { PF_NR = 2, PF_TW = 4, PF_PD = 2, PF_PD_SMALL = 8, SK_PD = 8 };
+enum { PF_NR = 2, PF_TW = 4, PF_PD = 2 };
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    if (a->P <= 16 && sk_lds(a)) {  // decode-sized batches whose terms fit LDS
+    if (a->P <= 32) {  // decode-sized batches: the skinny matmul streams every weight once
         const dim3 g((a->rows + 15) / 16);
-        const size_t lds = sk_lds(a);
-        if (a->il) {
-            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_sk_gemm<QMH_Q4, 2, SK_PD>), g, dim3(SK_WG), lds, s, *a);
-            else hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, 2, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+        const int nm = a->il ? 2 : 1;
+        const size_t lds = (size_t)sk_round(a->nb, nm, a->P) * nm * 16 * a->P * sizeof(float);
+#define SK_LAUNCH(NMV, TTV, PDV)                                                                              \
+    do {                                                                                                      \
+        if (a->dtype == QMH_Q4)                                                                               \
+            hipLaunchKernelGGL((k_sk_gemm<QMH_Q4, NMV, TTV, PDV>), g, dim3(SK_WG), lds, s, *a);               \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, NMV, TTV, PDV>), g, dim3(SK_WG), lds, s, *a);               \
+    } while (0)
+        if (a->P <= 16) {
+            if (a->il) SK_LAUNCH(2, 1, 8);
+            else SK_LAUNCH(1, 1, 6);
         } else {
-            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_sk_gemm<QMH_Q4, 1, SK_PD>), g, dim3(SK_WG), lds, s, *a);
-            else hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, 1, SK_PD>), g, dim3(SK_WG), lds, s, *a);
+            if (a->il) SK_LAUNCH(2, 2, 4);
+            else SK_LAUNCH(1, 2, 8);
         }
-        return (int)hipGetLastError();
-    }
-    if (a->P <= 16) {  // decode-sized batches: one 16-row x 16-token tile per wave, twice the waves,
-                       // deeper prefetch (the stream is latency-bound, not MFMA-bound)
-        const dim3 g(1, (a->rows + 63) / 64);
-        if (a->il) {
-            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 2, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
-            else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 2, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
-        } else {
-            if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 1, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
-            else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 1, 1, 1, PF_PD_SMALL>), g, dim3(QMH_WG), 0, s, *a);
-        }
+#undef SK_LAUNCH
         return (int)hipGetLastError();
     }
     // token groups past P are not launched; 16 * PF_TW divides PP, so every B load stays in the
