@@ -46,10 +46,11 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_softmax(float *att, const int32_t
     __shared__ float redf[16];
     const int h = blockIdx.x, b = blockIdx.y, n = pos_arr[b] + 1;
     float *x = att + ((size_t)b * n_heads + h) * max_seq;
+    const float x0 = x[0];  // read before any thread overwrites it with its exponential
     float m = -__builtin_inff();
     for (int t = threadIdx.x; t < n; t += QMH_WG) m = x[t] > m ? x[t] : m;
     m = qmh_block_max(m, redf);
-    if (x[0] != x[0]) m = x[0];  // the reference's scan starts from x[0]: a NaN there stays
+    if (x0 != x0) m = x0;  // the reference's scan starts from x[0]: a NaN there stays
     double sum = 0.0;
     for (int t = threadIdx.x; t < n; t += QMH_WG) {
         const float e = qmh_expf(x[t] - m);
@@ -116,14 +117,115 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_pv(const float *__restrict__ att,
     if (tid < hd) out[(size_t)b * n_heads * hd + h * hd + tid] = acc;
 }
 
+// The three steps above in one workgroup per (head blockIdx.x, sequence blockIdx.y), for contexts
+// of at most BT_FUSE_MAX positions: the scores and then the probabilities stay in LDS (P), V
+// passes through LDS BT_FC positions at a time (chunk 0 is loaded before the scores start, chunk
+// c+1 while chunk c is added). The sums are the same chains in the same order.
+constexpr int BT_T = 1024;
+constexpr int BT_FC = 128;
+constexpr int BT_FUSE_MAX = 16384;
+__global__ __launch_bounds__(BT_T) void k_bt_attn(const float *__restrict__ Q, const float *__restrict__ Kt,
+                                                  const float *__restrict__ V, long long kv_stride,
+                                                  const int32_t *__restrict__ pos_arr, float *out, int n_heads,
+                                                  int n_kv, int hd, int max_seq, float scale) {
+    extern __shared__ __align__(16) float bt_smem[];
+    float *vs = bt_smem;               // [BT_FC][128] staged V rows
+    float *P = bt_smem + BT_FC * 128;  // [n] scores, exponentials, probabilities
+    __shared__ float qs[128];
+    __shared__ float redf[BT_T / 64];
+    __shared__ double red[BT_T / 64 + 1];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, n = pos_arr[b] + 1;
+    const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, hd4 = hd >> 2;
+    const float *vbase = V + (size_t)b * kv_stride + (size_t)kvh * hd;
+    constexpr int VR = BT_FC * 32 / BT_T;  // float4 slots per thread per chunk (32 per row)
+    float4 vr[VR];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * BT_T + tid, t = e >> 5, c4 = e & 31;
+            const int tc = c0 + t < n ? c0 + t : n - 1;
+            vr[k] = c4 < hd4 ? *(const float4 *)(vbase + (size_t)tc * kvd + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load(0);
+    if (tid < hd) qs[tid] = Q[(size_t)b * n_heads * hd + h * hd + tid];
+    __syncthreads();
+    // scores: position t is lane t's chain over head_dim (64 K loads in flight)
+    const float *kc = Kt + (size_t)b * kv_stride + (size_t)kvh * hd * max_seq;
+    for (int t0 = 0; t0 < n; t0 += BT_T) {
+        if (t0 + (tid & ~63) >= n) break;  // whole wave past the context
+        const int t = t0 + tid, tc = t < n ? t : n - 1;
+        float s = 0.0f;
+        for (int d0 = 0; d0 < hd; d0 += 64) {
+            float kv[64];
+#pragma unroll
+            for (int j = 0; j < 64; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq + tc];
+#pragma unroll
+            for (int j = 0; j < 64; j++)
+                if (d0 + j < hd) s = s + qs[d0 + j] * kv[j];
+        }
+        if (t < n) P[t] = s * scale;
+    }
+    __syncthreads();
+    // softmax (src/ops.c:100-112) as k_bt_softmax
+    const float x0 = P[0];  // read before any thread overwrites it with its exponential
+    float m = -__builtin_inff();
+    for (int t = tid; t < n; t += BT_T) m = P[t] > m ? P[t] : m;
+    m = qmh_block_max(m, redf);
+    if (x0 != x0) m = x0;
+    double sum = 0.0;
+    for (int t = tid; t < n; t += BT_T) {
+        const float e = qmh_expf(P[t] - m);
+        P[t] = e;
+        sum += (double)e;
+    }
+    sum = qmh_block_sum_d(sum, red);
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
+        if (tid == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)P[t];
+            red[BT_T / 64] = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(red[BT_T / 64]);
+    }
+    for (int t = tid; t < n; t += BT_T) P[t] = P[t] * inv;
+    // P·V: lane i < hd runs column i's chain over the staged chunks
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += BT_FC) {
+        __syncthreads();  // P final (first chunk); the previous chunk's reads done
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * BT_T + tid;
+            *(float4 *)(vs + (e >> 5) * 128 + 4 * (e & 31)) = vr[k];
+        }
+        if (c0 + BT_FC < n) load(c0 + BT_FC);
+        __syncthreads();
+        if (tid < hd) {
+            const int nt = min(BT_FC, n - c0);
+            const float *pc = P + c0;
+            for (int t = 0; t < nt; t++) acc = acc + pc[t] * vs[t * 128 + tid];
+        }
+    }
+    if (tid < hd) out[(size_t)b * n_heads * hd + h * hd + tid] = acc;
+}
+
 }  // namespace
 
 extern "C" int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride,
                                        const int32_t *pos, int max_pos, float *att, float *out, int B, int n_heads,
-                                       int n_kv, int hd, int max_seq, float scale, void *stream) {
+                                       int n_kv, int hd, int max_seq, float scale, int split, void *stream) {
     if (B < 1 || hd < 4 || hd > 128 || hd % 4 || n_kv < 1 || n_heads % n_kv || max_pos < 0 || max_pos >= max_seq)
         return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
+    if (!split && max_pos < BT_FUSE_MAX) {
+        const size_t lds = (size_t)(BT_FC * 128 + max_pos + 1) * sizeof(float);
+        hipLaunchKernelGGL(k_bt_attn, dim3(n_heads, B), dim3(BT_T), lds, s, Q, Kt, V, kv_stride, pos, out, n_heads,
+                           n_kv, hd, max_seq, scale);
+        return (int)hipGetLastError();
+    }
     const int nz = max_pos / QMH_WG + 1;
     hipLaunchKernelGGL(k_bt_scores, dim3(n_heads, B, nz), dim3(QMH_WG), 0, s, Q, Kt, kv_stride, pos, att, n_heads,
                        n_kv, hd, max_seq, scale);

@@ -117,10 +117,12 @@ int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, flo
 /* attention of B independent sequences, one query each (src/model.c:127-156 per sequence): sequence b
  * at position pos[b] (device), query Q[b][n_heads*hd], caches Kt + b*kv_stride ([kvd][max_seq]) and
  * V + b*kv_stride ([max_seq][kvd]); att: scratch [B][n_heads][max_seq]; out[b][n_heads*hd].
- * max_pos: the largest pos[b] (sizes the grid). */
+ * max_pos: the largest pos[b] (sizes the grid and the LDS). split == 0: one fused kernel when
+ * max_pos < 16384 (att unused), else three launches through att; split != 0: always three launches
+ * (same results; kept selectable so both paths stay tested). */
 int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride, const int32_t *pos,
                             int max_pos, float *att, float *out, int B, int n_heads, int n_kv, int hd, int max_seq,
-                            float scale, void *stream);
+                            float scale, int split, void *stream);
 
 /* per row b of logits[B][V]: tok[b] = first argmax, pos[b] += 1, record[step*B + b] = it (if record) */
 int qmh_launch_bt_argmax(const float *logits, int B, int V, int32_t *tok, int32_t *pos, int32_t *record, int step,

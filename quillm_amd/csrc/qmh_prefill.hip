@@ -427,9 +427,9 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
         for (int k = 0; k < NPAIR; k++) {
             const int c = threadIdx.x + k * SK_WG, row = c & 15, p = c >> 4;
             if (p < P)
+                for (int jb = 0; jb < nr; jb++)  // the matrices' chains side by side, each in block order
 #pragma unroll
-                for (int m = 0; m < NM; m++)
-                    for (int jb = 0; jb < nr; jb++) s[k][m] = s[k][m] + T[(((size_t)m * rblk + jb) * 16 + row) * P + p];
+                    for (int m = 0; m < NM; m++) s[k][m] = s[k][m] + T[(((size_t)m * rblk + jb) * 16 + row) * P + p];
         }
         __syncthreads();
     }
@@ -462,7 +462,11 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
         else                                                                                                  \
             hipLaunchKernelGGL((k_sk_gemm<QMH_Q8, NMV, TTV, PDV>), g, dim3(SK_WG), lds, s, *a);               \
     } while (0)
-        if (a->P <= 16) {
+        // load depths timed on MI355X over the 7B shapes: for W1 | W3 up to 4 tokens, 3 blocks
+        // ahead (113 VGPRs: two workgroups per CU) beat 8 by 5%; from 5 tokens 8 is ahead
+        if (a->P <= 4 && a->il) {
+            SK_LAUNCH(2, 1, 3);
+        } else if (a->P <= 16) {
             if (a->il) SK_LAUNCH(2, 1, 8);
             else SK_LAUNCH(1, 1, 6);
         } else {

@@ -892,7 +892,7 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     LCHK(qmh_launch_pf_gemm(&a, s));
     if (bt)
         LCHK(qmh_launch_bt_attention(m->d_pf_q, kl, vl, bt->kv_stride, bt->pos, bt->max_pos, m->d_pf_att, m->d_pf_xb,
-                                     P, c->n_heads, c->n_kv_heads, m->hd, S_, 1.0f / sqrtf((float)m->hd), s));
+                                     P, c->n_heads, c->n_kv_heads, m->hd, S_, 1.0f / sqrtf((float)m->hd), 0, s));
     else
         LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads,
                                      m->hd, S_, 1.0f / sqrtf((float)m->hd), s));

@@ -92,3 +92,69 @@ def test_batch_errors(gpu, small_models):
     with gpu.Model.load(small_models[("small", "f32")]) as m:
         with pytest.raises(gpu.QmhError):
             gpu.Batch(m, 2)  # f32 weights have no batched matmul path
+
+
+def attention_reference(oracle, q, kt, v, n, n_kv, hd, scale):
+    """One sequence's attention (src/model.c:127-156) in float32 single operations: each score the
+    serial chain over head_dim times the scale, the oracle's softmax, each output element the chain
+    +0 + p_0 v_0[i] + p_1 v_1[i] + ... in position order."""
+    H = q.size // hd
+    out = np.zeros(H * hd, np.float32)
+    for h in range(H):
+        kvh = h // (H // n_kv)
+        s = np.zeros(n, np.float32)
+        for d in range(hd):
+            s = s + q[h * hd + d] * kt[kvh * hd + d, :n]
+        p = oracle.softmax(s * np.float32(scale))
+        acc = np.zeros(hd, np.float32)
+        for t in range(n):
+            acc = acc + p[t] * v[t, kvh * hd:(kvh + 1) * hd]
+        out[h * hd:(h + 1) * hd] = acc
+    return out
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,positions", [
+    (4, 4, 64, [0, 127, 128, 129]),
+    (8, 2, 128, [1023, 1024, 1025, 5]),
+    (6, 3, 96, [255, 700, 2047]),
+    (2, 1, 4, [0, 1, 300]),
+])
+def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positions):
+    """The fused attention kernel and the three-launch path it replaces up to 16384 positions give
+    the same bits, and both the float32 restatement's; positions straddle the V chunk (128) and
+    the thread count (1024)."""
+    import ctypes
+    say("batch attention", n_heads, n_kv, hd, positions)
+    L = gpu.load_library()
+    B, S = len(positions), max(positions) + 3
+    kvd = n_kv * hd
+    rs = np.random.default_rng(n_heads * 1000 + hd)
+    q = (rs.standard_normal((B, n_heads * hd)) * 0.7).astype(np.float32)
+    kt = (rs.standard_normal((B, kvd, S)) * 0.7).astype(np.float32)
+    v = rs.standard_normal((B, S, kvd)).astype(np.float32)
+    pos = np.array(positions, np.int32)
+    scale = 1.0 / np.sqrt(np.float32(hd))
+    bufs = [gpu.DeviceBuffer.from_array(a) for a in (q, kt, v, pos)]
+    att = gpu.DeviceBuffer(B * n_heads * S * 4)
+    outs = []
+    try:
+        fn = L.qmh_launch_bt_attention
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                              ctypes.c_void_p] + [ctypes.c_int] * 5 + [ctypes.c_float,
+                                                                                      ctypes.c_int, ctypes.c_void_p]
+        for split in (0, 1):
+            o = gpu.DeviceBuffer(B * n_heads * hd * 4)
+            rc = fn(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, kvd * S, bufs[3].ptr, int(pos.max()), att.ptr, o.ptr, B,
+                    n_heads, n_kv, hd, S, float(scale), split, L.qmh_stream())
+            assert rc == 0
+            gpu.sync()
+            outs.append(o.to_array(np.float32).reshape(B, n_heads * hd))
+            o.free()
+    finally:
+        for b in bufs + [att]:
+            b.free()
+    assert np.array_equal(bits(outs[0]), bits(outs[1])), "fused and split paths differ"
+    for b in range(B):
+        want = attention_reference(oracle, q[b], kt[b], v[b], int(pos[b]) + 1, n_kv, hd, scale)
+        assert np.array_equal(bits(outs[0][b]), bits(want)), f"sequence {b} (pos {pos[b]})"
