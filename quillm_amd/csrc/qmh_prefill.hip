@@ -499,30 +499,36 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
 __global__ __launch_bounds__(QMH_WG) void k_pf_scores(const float *__restrict__ Q, const float *__restrict__ Kt,
                                                       float *att, int P, int pos0, int n_heads, int n_kv, int hd,
                                                       int max_seq, float scale) {
-    __shared__ float qs[QMH_PF_TOK * 256];  // [token][d], hd <= 256
     const int h = blockIdx.x, g = blockIdx.y, t = blockIdx.z * QMH_WG + threadIdx.x;
     const int p0 = g * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
     if (blockIdx.z * QMH_WG > pos0 + p0 + np - 1) return;  // past every token of the group
     const int kvh = h / (n_heads / n_kv), D = n_heads * hd;
-    for (int i = threadIdx.x; i < QMH_PF_TOK * hd; i += QMH_WG) {
-        const int k = i / hd, d = i - k * hd;
-        qs[i] = k < np ? Q[(size_t)(p0 + k) * D + h * hd + d] : 0.0f;
-    }
-    __syncthreads();
+    // the group's queries, read with uniform (scalar) loads: every lane needs the same values.
+    // Tokens past P read the last token's row (their scores are never stored).
+    const float *qg = Q + (size_t)h * hd;
     const int tc = t < max_seq ? t : max_seq - 1;
     const float *kc = Kt + (size_t)kvh * hd * max_seq + tc;
     float s[QMH_PF_TOK];
 #pragma unroll
     for (int k = 0; k < QMH_PF_TOK; k++) s[k] = 0.0f;
-    for (int d0 = 0; d0 < hd; d0 += 8) {
-        float kv[8];
+    // 64 K values of the lane's position in flight, then four dimensions per step (hd is a
+    // multiple of 4)
+    for (int d0 = 0; d0 < hd; d0 += 64) {
+        float kv[64];
 #pragma unroll
-        for (int j = 0; j < 8; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
+        for (int j = 0; j < 64; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < 64; j += 4)
             if (d0 + j < hd) {
 #pragma unroll
-                for (int k = 0; k < QMH_PF_TOK; k++) s[k] = s[k] + qs[k * hd + d0 + j] * kv[j];
+                for (int k = 0; k < QMH_PF_TOK; k++) {
+                    const float *qk = qg + (size_t)(p0 + k < P ? p0 + k : P - 1) * D + d0 + j;
+                    const float4 q4 = make_float4(qk[0], qk[1], qk[2], qk[3]);
+                    s[k] = s[k] + q4.x * kv[j];
+                    s[k] = s[k] + q4.y * kv[j + 1];
+                    s[k] = s[k] + q4.z * kv[j + 2];
+                    s[k] = s[k] + q4.w * kv[j + 3];
+                }
             }
     }
 #pragma unroll
@@ -530,50 +536,53 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_scores(const float *__restrict__ 
         if (k < np && t <= pos0 + p0 + k) att[((size_t)h * P + p0 + k) * max_seq + t] = s[k] * scale;
 }
 
-// softmax of one (head, token) row in place (src/ops.c:100-112), as the decode kernels
+// softmax of one (head, token) row in place (src/ops.c:100-112), one wave per row (4 rows per
+// workgroup): the max and the double sum of the exponentials by shuffles, no barrier. The final
+// pass recomputes each exponential instead of storing and re-reading it (the same bits), so the
+// serial fallback of the sum works from the untouched scores.
 __global__ __launch_bounds__(QMH_WG) void k_pf_softmax(float *att, int P, int pos0, int max_seq) {
-    __shared__ double red[16];
-    __shared__ float redf[16];
-    const int h = blockIdx.x, p = blockIdx.y, n = pos0 + p + 1;
+    const int h = blockIdx.x, p = blockIdx.y * (QMH_WG / 64) + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (p >= P) return;  // the whole wave
+    const int n = pos0 + p + 1;
     float *x = att + ((size_t)h * P + p) * max_seq;
+    const float x0 = x[0];
     float m = -__builtin_inff();
-    for (int t = threadIdx.x; t < n; t += QMH_WG) m = x[t] > m ? x[t] : m;
-    m = qmh_block_max(m, redf);
-    if (x[0] != x[0]) m = x[0];  // the reference's scan starts from x[0]: a NaN there stays
+    for (int t = lane; t < n; t += 64) m = x[t] > m ? x[t] : m;
+    m = qmh_wave_max(m);
+    if (x0 != x0) m = x0;  // the reference's scan starts from x[0]: a NaN there stays
     double sum = 0.0;
-    for (int t = threadIdx.x; t < n; t += QMH_WG) {
-        const float e = qmh_expf(x[t] - m);
-        x[t] = e;
-        sum += (double)e;
-    }
-    sum = qmh_block_sum_d(sum, red);
+    for (int t = lane; t < n; t += 64) sum += (double)qmh_expf(x[t] - m);
+    sum = qmh_wave_sum_d(sum);
     const double d = qmh_sum_slack(sum, n);
     float inv = qmh_recip_of_sum(sum - d);
     if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
-        if (threadIdx.x == 0) {
-            double ser = 0.0;
-            for (int t = 0; t < n; t++) ser += (double)x[t];
-            red[8] = ser;
-        }
-        __syncthreads();
-        inv = qmh_recip_of_sum(red[8]);
+        double ser = 0.0;
+        if (lane == 0)
+            for (int t = 0; t < n; t++) ser += (double)qmh_expf(x[t] - m);
+        inv = qmh_recip_of_sum(__shfl(ser, 0));
     }
-    for (int t = threadIdx.x; t < n; t += QMH_WG) x[t] = x[t] * inv;
+    for (int t = lane; t < n; t += 64) x[t] = qmh_expf(x[t] - m) * inv;
 }
 
 // out[token][h*hd + i] = +0 + p_0 v_0[i] + p_1 v_1[i] + ... in position order (src/model.c:147-154);
 // one workgroup per (head, 16 tokens), head_dim <= 128. V and the probabilities pass through LDS
 // in chunks of 64 positions (cooperative float4 loads, the next chunk's held in registers while
 // the current one is used); thread (i, half) runs column i's chains of tokens 8*half .. +7.
+// The probabilities sit in LDS as [position][token], so a thread's 8 per position are two
+// 16-byte reads. Positions up to pos0 + p0 are seen by every token of the group and run four at a
+// time with no mask; the last 15 positions of the group (its causal diagonal) extend only the
+// chains of the tokens that see them (a select, never an added zero: that would turn -0 into +0
+// and propagate a NaN from V).
 #define QMH_PF_VC 64
 __global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att, const float *__restrict__ V,
                                                   float *out, int P, int pos0, int n_heads, int n_kv, int hd,
                                                   int max_seq) {
-    __shared__ __align__(16) float ps[QMH_PF_TOK * QMH_PF_VC];  // [token][t]
+    __shared__ __align__(16) float ps[QMH_PF_VC * QMH_PF_TOK];  // [t][token]
     __shared__ __align__(16) float vs[QMH_PF_VC * 128];         // [t][column]
     const int h = blockIdx.x, p0 = blockIdx.y * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
     const int kvh = h / (n_heads / n_kv), kvd = hd * n_kv, tid = threadIdx.x;
     const int tmax = pos0 + p0 + np;  // positions 0 .. tmax-1 are used by some token
+    const int tall = pos0 + p0 + 1;   // positions 0 .. tall-1 are used by every token of the group
     const float *vbase = V + (size_t)kvh * hd;
     const int hd4 = hd >> 2;
     constexpr int VR = QMH_PF_VC * 128 / 4 / QMH_WG;     // float4 of V per thread per chunk
@@ -606,18 +615,47 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att,
             *(float4 *)(vs + (e >> 5) * 128 + 4 * (e & 31)) = vr[k];
         }
 #pragma unroll
-        for (int k = 0; k < PR; k++) ps[k * QMH_WG + tid] = pr[k];
+        for (int k = 0; k < PR; k++) {
+            const int e = k * QMH_WG + tid;
+            ps[(e % QMH_PF_VC) * QMH_PF_TOK + e / QMH_PF_VC] = pr[k];
+        }
         if (c0 + QMH_PF_VC < tmax) load(c0 + QMH_PF_VC);
         __syncthreads();
         if (i < hd) {
             const int nt = min(QMH_PF_VC, tmax - c0);
-            for (int t = 0; t < nt; t++) {
+            const int nall = min(nt, max(tall - c0, 0));  // positions of this chunk every token sees
+            const float *pp = ps + 8 * half;
+            int t = 0;
+            for (; t + 4 <= nall; t += 4) {
+                float v[4];
+                float4 pa[4], pb[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    v[u] = vs[(t + u) * 128 + i];
+                    pa[u] = *(const float4 *)(pp + (t + u) * QMH_PF_TOK);
+                    pb[u] = *(const float4 *)(pp + (t + u) * QMH_PF_TOK + 4);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    acc[0] = acc[0] + pa[u].x * v[u];
+                    acc[1] = acc[1] + pa[u].y * v[u];
+                    acc[2] = acc[2] + pa[u].z * v[u];
+                    acc[3] = acc[3] + pa[u].w * v[u];
+                    acc[4] = acc[4] + pb[u].x * v[u];
+                    acc[5] = acc[5] + pb[u].y * v[u];
+                    acc[6] = acc[6] + pb[u].z * v[u];
+                    acc[7] = acc[7] + pb[u].w * v[u];
+                }
+            }
+            for (; t < nt; t++) {
                 const float v = vs[t * 128 + i];
+                const float4 pa = *(const float4 *)(pp + t * QMH_PF_TOK), pb = *(const float4 *)(pp + t * QMH_PF_TOK + 4);
+                const float pk[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
                 const int kmin = c0 + t - (pos0 + p0);  // tokens kk >= kmin see position c0 + t
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
-                    const int kk = 8 * half + k;
-                    if (kk >= kmin) acc[k] = acc[k] + ps[kk * QMH_PF_VC + t] * v;
+                    const float nx = acc[k] + pk[k] * v;
+                    acc[k] = 8 * half + k >= kmin ? nx : acc[k];
                 }
             }
         }
@@ -638,7 +676,8 @@ extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const fl
     const int ng = (P + QMH_PF_TOK - 1) / QMH_PF_TOK, nz = (pos0 + P + QMH_WG - 1) / QMH_WG;
     hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
                        hd, max_seq, scale);
-    hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, P), dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
+    hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, (P + QMH_WG / 64 - 1) / (QMH_WG / 64)), dim3(QMH_WG), 0, s, att, P, pos0,
+                       max_seq);
     hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd, max_seq);
     return (int)hipGetLastError();
 }
