@@ -501,7 +501,9 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_scores(const float *__restrict__ 
                                                       int max_seq, float scale) {
     const int h = blockIdx.x, g = blockIdx.y, t = blockIdx.z * QMH_WG + threadIdx.x;
     const int p0 = g * QMH_PF_TOK, np = min(QMH_PF_TOK, P - p0);
-    if (blockIdx.z * QMH_WG > pos0 + p0 + np - 1) return;  // past every token of the group
+    // a wave whose 64 positions are all past the group's last token has nothing to store (the
+    // kernel has no barrier, so waves leave independently)
+    if ((int)(blockIdx.z * QMH_WG + (threadIdx.x & ~63u)) > pos0 + p0 + np - 1) return;
     const int kvh = h / (n_heads / n_kv), D = n_heads * hd;
     // the group's queries, read with uniform (scalar) loads: every lane needs the same values.
     // Tokens past P read the last token's row (their scores are never stored).
