@@ -441,6 +441,172 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
     }
 }
 
+// ============================================================================ multi-token matvec
+//
+// Up to BMV_P tokens (batched decode, short prompts): the decode matvec's organisation with one
+// record and one term per token. A workgroup owns a contiguous range of whole tiles (contiguous
+// slots: tile-major, then block, then row in tile). Its threads stream every slot once (BMV_U slots per
+// thread in flight, two register sets), and for each token form the block's exact int32 dot with
+// sdot4 against that token's activation record in LDS, then the term (float)acc * (dw * dx) into LDS
+// at [token][slot]. After the stream one lane per (row, token) walks its terms in block order from
+// +0 (the reference's chain) and runs the prefill epilogue (pf_store).
+//
+// Records: 48 bytes per (block, token) built from the Q8_0 image of k_pf_quant, codes in the order
+// the weights pair with (Q8_0: element order; Q4_0: even elements, then odd: the image's perm8
+// groups [e0 e2 e4 e6 e1 e3 e5 e7] give their first 4 bytes to the even half and the last 4 to the
+// odd half), then d (fp32), then the code sum (Q4_0: sum (q - 8) x = sum q x - 8 sum x, exact).
+#define BMV_P 4
+#define BMV_NT 512
+#define BMV_REC 48
+#define BMV_LDS (160 * 1024)
+__host__ __device__ inline int bmv_ntiles(const qmh_pf_args &a) {
+    return a.il ? a.rows_alloc / (a.tile_r / 2) : a.rows_alloc / a.tile_r;
+}
+__host__ __device__ inline int bmv_tile0(int w, int ntiles, int G) { return (int)((long long)w * ntiles / G); }
+
+template <int WT>
+__global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
+    constexpr int CB = WT == QMH_Q8 ? 32 : 16;  // code bytes per slot
+    constexpr int NV = CB / 16;
+    constexpr int U = WT == QMH_Q8 ? 4 : 8;      // slots per thread per register set
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, P = a.P, nb = a.nb, R = a.tile_r, lgR = __builtin_ctz((unsigned)R);
+    const int ntiles = bmv_ntiles(a);
+    const int t0 = bmv_tile0(blockIdx.x, ntiles, gridDim.x), t1 = bmv_tile0(blockIdx.x + 1, ntiles, gridDim.x);
+    const int ntw = t1 - t0;
+    if (ntw <= 0) return;  // the host launches at most ntiles workgroups
+    const int TS = ntw * nb * R;  // slots of the range
+    float *T = (float *)(smem + (size_t)nb * P * BMV_REC);
+    const uint8_t *cbase = a.codes + (size_t)t0 * nb * R * CB;
+    const uint16_t *sbase = a.scales + (size_t)t0 * nb * R;
+
+    // slot l = j*BMV_NT + tid of the range: block column (l >> lgR) = (tid >> lgR) + j*(BMV_NT >> lgR);
+    // its block index is that mod nb, kept incrementally (step < nb)
+    const int nper = (TS + BMV_NT - 1) / BMV_NT;
+    const int bstep = (BMV_NT >> lgR) % nb;
+    uint4 cA[U][NV], cB[U][NV];
+    uint32_t sA[U], sB[U];
+    auto load = [&](uint4 (&c)[U][NV], uint32_t (&sc)[U], int j0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int l0 = (j0 + u) * BMV_NT + tid, l = l0 < TS ? l0 : TS - 1;
+#pragma unroll
+            for (int v = 0; v < NV; v++) c[u][v] = *(const uint4 *)(cbase + (size_t)l * CB + 16 * v);
+            sc[u] = sbase[l];
+        }
+    };
+    load(cA, sA, 0);
+
+    // records
+    const int nitems = nb * P * 4;  // (block, token, 8-byte group); groups of one record in adjacent lanes
+    for (int i0 = 0; i0 < nitems; i0 += BMV_NT) {
+        const int it = i0 + tid, g = it & 3, bp = it >> 2, b = bp / P, p = bp - b * P;
+        const bool ok = it < nitems;
+        int2 v = make_int2(0, 0);
+        if (ok) v = *(const int2 *)(a.xc + ((size_t)b * a.PP + p) * 32 + 8 * g);
+        int sum = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
+        sum = __builtin_amdgcn_sdot4(v.y, 0x01010101, sum, false);
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        if (ok) {
+            uint8_t *rec = smem + (size_t)bp * BMV_REC;
+            if (WT == QMH_Q4) {
+                *(int *)(rec + 4 * g) = v.x;
+                *(int *)(rec + 16 + 4 * g) = v.y;
+            } else {
+                *(int2 *)(rec + 8 * g) = v;
+            }
+            if (g == 0) {
+                *(float *)(rec + 32) = a.xd[(size_t)b * a.PP + p];
+                *(int *)(rec + 36) = sum;
+            }
+        }
+    }
+    __syncthreads();
+
+    // the stream
+    int bcur = (tid >> lgR) % nb;
+    auto compute = [&](const uint4 (&c)[U][NV], const uint32_t (&sc)[U], int j0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int l = (j0 + u) * BMV_NT + tid;
+            if (j0 + u < nper) {  // uniform
+                const float dw = qmh_h2f((uint16_t)sc[u]);
+#pragma unroll
+                for (int p = 0; p < BMV_P; p++)
+                    if (p < P) {
+                        const uint8_t *rp = smem + (size_t)(bcur * P + p) * BMV_REC;
+                        const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);
+                        const float2 ds = *(const float2 *)(rp + 32);
+                        int acc;
+                        if (WT == QMH_Q4) {
+                            const uint4 w = c[u][0];
+                            acc = -8 * __float_as_int(ds.y);
+                            acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);
+                        } else {
+                            const uint4 w0 = c[u][0], w1 = c[u][NV - 1];
+                            acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, 0, false);
+                            acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);
+                            acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);
+                        }
+                        if (l < TS) T[(size_t)p * TS + l] = (float)acc * (dw * ds.x);
+                    }
+            }
+            bcur += bstep;
+            bcur -= bcur >= nb ? nb : 0;
+        }
+    };
+    for (int j0 = 0; j0 < nper; j0 += 2 * U) {
+        if (j0 + U < nper) load(cB, sB, j0 + U);
+        compute(cA, sA, j0);
+        if (j0 + 2 * U < nper) load(cA, sA, j0 + 2 * U);
+        if (j0 + U < nper) compute(cB, sB, j0 + U);
+    }
+    __syncthreads();
+
+    // chains and epilogues: pair c = p*rows_w + i (row i of the range: tile i >> lgR, row i & (R-1));
+    // a tile's rows are consecutive lanes of one wave (R divides 64, rows_w is a multiple of R)
+    const int rows_w = ntw * R, npair = rows_w * P;
+    for (int c0 = 0; c0 < npair; c0 += BMV_NT) {
+        const int c = c0 + tid, p = c / rows_w, i = c - p * rows_w, tl = i >> lgR, r = i & (R - 1);
+        float y = 0.0f;
+        if (c < npair) {
+            const float *tp = T + (size_t)p * TS + (size_t)tl * nb * R + r;
+            int b = 0;
+            for (; b + 16 <= nb; b += 16) {
+                float v[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = tp[(b + k) * R];
+#pragma unroll
+                for (int k = 0; k < 16; k++) y = y + v[k];
+            }
+            for (; b < nb; b++) y = y + tp[b * R];
+        }
+        const int tile = t0 + tl;
+        if (a.il) {  // rows r < R/2 of a tile are W1 rows, r + R/2 their W3 rows
+            const float up = __shfl_down(y, R >> 1);
+            const int row = tile * (R >> 1) + r;
+            if (c < npair && r < (R >> 1) && row < a.rows) pf_store(a, row, p, y, up, 0.0f);
+        } else {
+            const float partner = __shfl_xor(y, 1);  // row ^ 1: RoPE's pair
+            const int row = tile * R + r;
+            if (c < npair && row < a.rows) pf_store(a, row, p, y, y, partner);
+        }
+    }
+}
+
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
 // token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
 // more leave too few waves to cover the latency at P = 512.
@@ -451,6 +617,19 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
+    if (a->P <= BMV_P) {  // the multi-token matvec when one tile's terms fit its LDS with the records
+        const int ntiles = bmv_ntiles(*a);
+        const size_t rec = (size_t)a->nb * a->P * BMV_REC, per_tile = (size_t)a->P * a->tile_r * a->nb * sizeof(float);
+        if (rec + per_tile <= BMV_LDS) {
+            // whole tiles per workgroup: about one workgroup per CU (256), fewer tiles if LDS asks
+            const int fit = (int)((BMV_LDS - rec) / per_tile), want = ntiles / 256 > 1 ? ntiles / 256 : 1;
+            const int k = want < fit ? want : fit, G = (ntiles + k - 1) / k;
+            const size_t lds = rec + (size_t)((ntiles + G - 1) / G) * per_tile;
+            if (a->dtype == QMH_Q4) hipLaunchKernelGGL(k_bmv<QMH_Q4>, dim3(G), dim3(BMV_NT), lds, s, *a);
+            else hipLaunchKernelGGL(k_bmv<QMH_Q8>, dim3(G), dim3(BMV_NT), lds, s, *a);
+            return (int)hipGetLastError();
+        }
+    }
     if (a->P <= 32) {  // decode-sized batches: the skinny matmul streams every weight once
         const dim3 g((a->rows + 15) / 16);
         const int nm = a->il ? 2 : 1;
