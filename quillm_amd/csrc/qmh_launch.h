@@ -93,6 +93,13 @@ typedef struct {
     const int8_t *xc;
     const float *xd;
     int PP, P;
+    /* or (xf != NULL) the f32 rows they come from: xf[p*ldxf + i], i < nxf, RMSNorm'd with gain norm_w
+     * first when norm_w != NULL; the launcher quantizes them (inside the multi-token matvec, or into
+     * xc/xd with k_pf_quant before the matmul) */
+    const float *xf;
+    int ldxf, nxf;
+    const float *norm_w;
+    float eps;
     /* epilogue: out0 row-major [P][ld0]; QKV: q -> out0, k -> out1 ([kvd][max_seq]), v -> out2 */
     int epi;
     float *out0, *out1, *out2;

@@ -464,6 +464,58 @@ __host__ __device__ inline int bmv_ntiles(const qmh_pf_args &a) {
 }
 __host__ __device__ inline int bmv_tile0(int w, int ntiles, int G) { return (int)((long long)w * ntiles / G); }
 
+// Records straight from the f32 rows of a plain (not RMSNorm'd) input, as k_pf_quant computes them:
+// item k = p*nb + b is block b of token p, 8 lanes per item with 4 values each, four rounds of
+// items at a time. Q4_0 consumers get the split code order.
+template <int WT>
+__device__ __forceinline__ void bmv_quant_item(const qmh_pf_args &a, uint8_t *rec, int k, int nk, const float (&v)[4]) {
+    const int sub = threadIdx.x & 7, P = a.P, nb = a.nb, p = k / nb, b = k - p * nb;
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float av = fabsf(v[j]);
+        m = av > m ? av : m;
+    }
+    m = qmh_amax8(m);
+    const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
+    int q[4];
+    qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
+    const int qs = qmh_sum8(q[0] + q[1] + q[2] + q[3]);
+    if (k < nk) {
+        uint8_t *rp = rec + (size_t)(b * P + p) * BMV_REC;
+        if (WT == QMH_Q4) {  // elements 4s, 4s+2 at 2s, 2s+1; 4s+1, 4s+3 at 16+2s, 16+2s+1
+            *(uint16_t *)(rp + 2 * sub) = (uint16_t)((q[0] & 0xff) | (q[2] & 0xff) << 8);
+            *(uint16_t *)(rp + 16 + 2 * sub) = (uint16_t)((q[1] & 0xff) | (q[3] & 0xff) << 8);
+        } else {
+            *(uint32_t *)(rp + 4 * sub) =
+                (uint32_t)((q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (q[3] & 0xff) << 24);
+        }
+        if (sub == 0) {
+            *(float *)(rp + 32) = dd;
+            *(int *)(rp + 36) = qs;
+        }
+    }
+}
+
+template <int WT>
+__device__ __forceinline__ void bmv_records_f32(const qmh_pf_args &a, uint8_t *rec) {
+    const int tid = threadIdx.x, sub = tid & 7, P = a.P, nb = a.nb, n = a.nxf;
+    const int nk = P * nb, NR = (nk + BMV_NT / 8 - 1) / (BMV_NT / 8);
+    for (int r0 = 0; r0 < NR; r0 += 4) {  // uniform: DPP needs all 8 lanes of an item
+        float xv[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int k = (r0 + u) * (BMV_NT / 8) + (tid >> 3), p = k / nb, i0 = (k - p * nb) * 32 + 4 * sub;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                xv[u][j] = (r0 + u < NR && k < nk && i0 + j < n) ? a.xf[(size_t)p * a.ldxf + i0 + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (r0 + u < NR) bmv_quant_item<WT>(a, rec, (r0 + u) * (BMV_NT / 8) + (tid >> 3), nk, xv[u]);
+    }
+}
+
 template <int WT>
 __global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;  // code bytes per slot
@@ -497,7 +549,10 @@ __global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
     };
     load(cA, sA, 0);
 
-    // records
+    if (a.xf) {
+        bmv_records_f32<WT>(a, smem);
+    } else {
+    // records from the quantized image
     const int nitems = nb * P * 4;  // (block, token, 8-byte group); groups of one record in adjacent lanes
     for (int i0 = 0; i0 < nitems; i0 += BMV_NT) {
         const int it = i0 + tid, g = it & 3, bp = it >> 2, b = bp / P, p = bp - b * P;
@@ -521,6 +576,7 @@ __global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
                 *(int *)(rec + 36) = sum;
             }
         }
+    }
     }
     __syncthreads();
 
@@ -617,18 +673,29 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    if (a->P <= BMV_P) {  // the multi-token matvec when one tile's terms fit its LDS with the records
-        const int ntiles = bmv_ntiles(*a);
-        const size_t rec = (size_t)a->nb * a->P * BMV_REC, per_tile = (size_t)a->P * a->tile_r * a->nb * sizeof(float);
-        if (rec + per_tile <= BMV_LDS) {
-            // whole tiles per workgroup: about one workgroup per CU (256), fewer tiles if LDS asks
-            const int fit = (int)((BMV_LDS - rec) / per_tile), want = ntiles / 256 > 1 ? ntiles / 256 : 1;
-            const int k = want < fit ? want : fit, G = (ntiles + k - 1) / k;
-            const size_t lds = rec + (size_t)((ntiles + G - 1) / G) * per_tile;
-            if (a->dtype == QMH_Q4) hipLaunchKernelGGL(k_bmv<QMH_Q4>, dim3(G), dim3(BMV_NT), lds, s, *a);
-            else hipLaunchKernelGGL(k_bmv<QMH_Q8>, dim3(G), dim3(BMV_NT), lds, s, *a);
-            return (int)hipGetLastError();
-        }
+    if (a->xf && (a->nxf < 1 || a->nxf > 32 * a->nb || a->ldxf < a->nxf)) return (int)hipErrorInvalidValue;
+    // the multi-token matvec when one tile's terms fit its LDS with the records. It quantizes a plain
+    // input (Wo's, W2's) itself: timed on MI355X at 1-4 tokens, that saves 5-9 us per matmul over
+    // k_pf_quant's launch, while an RMSNorm'd input quantized in every workgroup was 6 us slower.
+    const int ntiles = bmv_ntiles(*a);
+    const size_t rec = (size_t)a->nb * a->P * BMV_REC, per_tile = (size_t)a->P * a->tile_r * a->nb * sizeof(float);
+    const bool bmv = a->P <= BMV_P && rec + per_tile <= BMV_LDS;
+    const bool fuse = bmv && a->xf && !a->norm_w;
+    if (a->xf && !fuse) {  // the quantized image first
+        const int rc = qmh_launch_pf_quant(a->xf, a->ldxf, a->norm_w, a->eps, a->nxf, a->P, (int8_t *)a->xc,
+                                           (float *)a->xd, a->PP, a->dtype == QMH_Q4, stream);
+        if (rc) return rc;
+    }
+    if (bmv) {
+        qmh_pf_args b = *a;
+        if (!fuse) b.xf = nullptr;
+        // whole tiles per workgroup: about one workgroup per CU (256), fewer tiles if LDS asks
+        const int fit = (int)((BMV_LDS - rec) / per_tile), want = ntiles / 256 > 1 ? ntiles / 256 : 1;
+        const int k = want < fit ? want : fit, G = (ntiles + k - 1) / k;
+        const size_t lds = rec + (size_t)((ntiles + G - 1) / G) * per_tile;
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL(k_bmv<QMH_Q4>, dim3(G), dim3(BMV_NT), lds, s, b);
+        else hipLaunchKernelGGL(k_bmv<QMH_Q8>, dim3(G), dim3(BMV_NT), lds, s, b);
+        return (int)hipGetLastError();
     }
     if (a->P <= 32) {  // decode-sized batches: the skinny matmul streams every weight once
         const dim3 g((a->rows + 15) / 16);

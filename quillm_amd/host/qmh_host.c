@@ -860,7 +860,7 @@ typedef struct {
  * pos.. in the model's caches, or (bt != NULL) one token of each of P independent sequences */
 static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipStream_t s) {
     const qmh_config *c = &m->cfg;
-    const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq, PP = m->pf_pp;
+    const int D = c->dim, H = c->hidden_dim, S_ = c->max_seq;
     dev_layer *L = &m->layers[l];
     float *kl = m->d_kt + (size_t)l * S_ * m->kvd, *vl = m->d_v + (size_t)l * S_ * m->kvd;
     if (bt) {
@@ -869,9 +869,12 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     }
     qmh_pf_args a;
     /* q, k, v = W rmsnorm(x); rope; k, v -> caches */
-    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * l) * D, c->norm_eps, D, P, m->d_pf_xc, m->d_pf_xd,
-                             PP, L->qkv.dtype == QMH_Q4_0, s));
     pf_args_for(m, &L->qkv, P, &a);
+    a.xf = m->d_pf_x;
+    a.ldxf = D;
+    a.nxf = D;
+    a.norm_w = m->d_norms + (size_t)(2 * l) * D;
+    a.eps = c->norm_eps;
     a.rows_alloc = L->qkv.ntiles * L->qkv.tile_r;
     a.epi = QMH_PF_QKV;
     a.out0 = m->d_pf_q;
@@ -897,17 +900,24 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
         LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads,
                                      m->hd, S_, 1.0f / sqrtf((float)m->hd), s));
     /* x += Wo xb */
-    LCHK(qmh_launch_pf_quant(m->d_pf_xb, D, NULL, 0.0f, D, P, m->d_pf_xc, m->d_pf_xd, PP, L->wo.dtype == QMH_Q4_0, s));
     pf_args_for(m, &L->wo, P, &a);
+    a.xf = m->d_pf_xb;
+    a.ldxf = D;
+    a.nxf = D;
+    a.norm_w = NULL;
+    a.eps = 0.0f;
     a.rows_alloc = L->wo.ntiles * L->wo.tile_r;
     a.epi = QMH_PF_ADD;
     a.out0 = m->d_pf_x;
     a.ld0 = D;
     LCHK(qmh_launch_pf_gemm(&a, s));
     /* hb = silu(W1 rmsnorm(x)) * (W3 rmsnorm(x)) */
-    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * l + 1) * D, c->norm_eps, D, P, m->d_pf_xc,
-                             m->d_pf_xd, PP, L->w13.dtype == QMH_Q4_0, s));
     pf_args_for(m, &L->w13, P, &a);
+    a.xf = m->d_pf_x;
+    a.ldxf = D;
+    a.nxf = D;
+    a.norm_w = m->d_norms + (size_t)(2 * l + 1) * D;
+    a.eps = c->norm_eps;
     a.il = 1;
     a.rows_alloc = L->w13.ntiles * (L->w13.tile_r / 2);
     a.epi = QMH_PF_SWIGLU;
@@ -915,8 +925,12 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     a.ld0 = H;
     LCHK(qmh_launch_pf_gemm(&a, s));
     /* x += W2 hb */
-    LCHK(qmh_launch_pf_quant(m->d_pf_hb, H, NULL, 0.0f, H, P, m->d_pf_xc, m->d_pf_xd, PP, L->w2.dtype == QMH_Q4_0, s));
     pf_args_for(m, &L->w2, P, &a);
+    a.xf = m->d_pf_hb;
+    a.ldxf = H;
+    a.nxf = H;
+    a.norm_w = NULL;
+    a.eps = 0.0f;
     a.rows_alloc = L->w2.ntiles * L->w2.tile_r;
     a.epi = QMH_PF_ADD;
     a.out0 = m->d_pf_x;
@@ -938,9 +952,12 @@ static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
             if (pf_layer(m, l, P, pos, NULL, g_stream)) return -1;
         if (logits) { /* logits = Woutput rmsnorm(x) for every position (src/model.c:188-189) */
             qmh_pf_args a;
-            LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * c->n_layers) * D, c->norm_eps, D, P,
-                                     m->d_pf_xc, m->d_pf_xd, m->pf_pp, m->output.dtype == QMH_Q4_0, g_stream));
             pf_args_for(m, &m->output, P, &a);
+            a.xf = m->d_pf_x;
+            a.ldxf = D;
+            a.nxf = D;
+            a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
+            a.eps = c->norm_eps;
             a.rows_alloc = m->output.ntiles * m->output.tile_r;
             a.epi = QMH_PF_STORE;
             a.out0 = m->d_pf_logits;
@@ -1071,9 +1088,12 @@ static int batch_step(qmh_batch *b, int max_pos, hipStream_t s) {
     for (int l = 0; l < c->n_layers; l++)
         if (pf_layer(m, l, B, 0, &bt, s)) return -1;
     qmh_pf_args a;
-    LCHK(qmh_launch_pf_quant(m->d_pf_x, D, m->d_norms + (size_t)(2 * c->n_layers) * D, c->norm_eps, D, B, m->d_pf_xc,
-                             m->d_pf_xd, m->pf_pp, m->output.dtype == QMH_Q4_0, s));
     pf_args_for(m, &m->output, B, &a);
+    a.xf = m->d_pf_x;
+    a.ldxf = D;
+    a.nxf = D;
+    a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
+    a.eps = c->norm_eps;
     a.rows_alloc = m->output.ntiles * m->output.tile_r;
     a.epi = QMH_PF_STORE;
     a.out0 = m->d_pf_logits;
