@@ -97,11 +97,12 @@ __device__ __forceinline__ void pf_quant_block(const float (&v)[4], int b, int n
 // One workgroup per token; 8 lanes per block, 4 values each. Rows of up to PQ_R*1024 values are
 // loaded once into registers (one round of loads), larger ones round by round.
 #define PQ_R 16
-__global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x, int ldx, const float *w, float eps,
+template <int NT>
+__global__ __launch_bounds__(NT) void k_pf_quant(const float *__restrict__ x, int ldx, const float *w, float eps,
                                                      int n, int8_t *xc, float *xd, int PP, int perm8) {
-    __shared__ double red[16];
+    __shared__ double red[NT / 64 + 1];  // the waves' partial sums, then the serial sum
     const int p = blockIdx.x, tid = threadIdx.x, nb = (n + 31) / 32, sub = tid & 7;
-    const int R = (nb + QMH_WG / 8 - 1) / (QMH_WG / 8);  // rounds of 32 blocks
+    const int R = (nb + NT / 8 - 1) / (NT / 8);  // rounds of 32 blocks
     const float *row = x + (size_t)p * ldx;
     const bool held = R <= PQ_R;
     float xv[PQ_R][4];
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
         for (int r = 0; r < PQ_R; r++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int i = (r * (QMH_WG / 8) + (tid >> 3)) * 32 + sub * 4 + j;
+                const int i = (r * (NT / 8) + (tid >> 3)) * 32 + sub * 4 + j;
                 xv[r][j] = (r < R && i < n) ? row[i] : 0.0f;
             }
         if (w)
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
 #pragma unroll
                 for (int j = 0; j < 4; j++) ss += (double)xv[r][j] * (double)xv[r][j];
     } else if (w) {
-        for (int i = tid; i < n; i += QMH_WG) ss += (double)row[i] * (double)row[i];
+        for (int i = tid; i < n; i += NT) ss += (double)row[i] * (double)row[i];
     }
     float inv = 1.0f;
     if (w) {
@@ -131,10 +132,10 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
             if (tid == 0) {
                 double s2 = 0.0;
                 for (int i = 0; i < n; i++) s2 += (double)row[i] * (double)row[i];
-                red[8] = s2;
+                red[NT / 64] = s2;
             }
             __syncthreads();
-            inv = qmh_rms_inv(red[8], n, eps);
+            inv = qmh_rms_inv(red[NT / 64], n, eps);
         }
     }
     // (x*inv)*w as the reference; rounds are uniform (DPP needs all 8 lanes of a block)
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
 #pragma unroll
         for (int r = 0; r < PQ_R; r++)
             if (r < R) {
-                const int b = r * (QMH_WG / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
+                const int b = r * (NT / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
                 float v[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++)
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
             }
     } else {
         for (int r = 0; r < R; r++) {
-            const int b = r * (QMH_WG / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
+            const int b = r * (NT / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
             float v[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -165,7 +166,14 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_quant(const float *__restrict__ x
 
 extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc,
                                    float *xd, int PP, int perm8, void *stream) {
-    hipLaunchKernelGGL(k_pf_quant, dim3(P), dim3(QMH_WG), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd, PP, perm8);
+    // a few rows (batched decode): 1024 threads per row, one round of loads for a 4096-value row
+    // and 16 waves to wait on them; many rows (prefill): 256 threads, more workgroups
+    if (P <= 16)
+        hipLaunchKernelGGL(k_pf_quant<1024>, dim3(P), dim3(1024), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd, PP,
+                           perm8);
+    else
+        hipLaunchKernelGGL(k_pf_quant<QMH_WG>, dim3(P), dim3(QMH_WG), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd,
+                           PP, perm8);
     return (int)hipGetLastError();
 }
 
