@@ -171,13 +171,17 @@ def main():
             sampled_s = time.perf_counter() - t0
         log(f"[bench] sampled decode {K} steps: {sampled_s * 1e3:.2f} ms wall, {K / sampled_s:.1f} tok/s")
 
-        # batched decode of 16 independent sequences (qmh_batch_greedy) over the same positions:
+        # batched decode of 4 and 16 independent sequences (qmh_batch_greedy) over the same positions:
         # informational, the metric stays batch 1
-        BB = 16
-        with q.Batch(m, BB) as bt:
-            bt.greedy([tok0] * BB, [P] * BB, 2)
-            _, b_ms = bt.greedy([tok0] * BB, [P] * BB, K)
-        log(f"[bench] batched decode B={BB}: {b_ms / K:.3f} ms per step, {BB * K / (b_ms / 1e3):.1f} tok/s aggregate")
+        batched = []
+        for BB in (4, 16):
+            with q.Batch(m, BB) as bt:
+                bt.greedy([tok0] * BB, [P] * BB, 2)
+                _, b_ms = bt.greedy([tok0] * BB, [P] * BB, K)
+            batched.append({"sequences": BB, "tok_s_aggregate": round(BB * K / (b_ms / 1e3), 1),
+                            "ms_per_step": round(b_ms / K, 3)})
+            log(f"[bench] batched decode B={BB}: {b_ms / K:.3f} ms per step, "
+                f"{BB * K / (b_ms / 1e3):.1f} tok/s aggregate")
 
         # dominant kernel: fused RMSNorm + W1|W3 matvec + SwiGLU, cycling the layers
         stages = {}
@@ -213,8 +217,7 @@ def main():
                    "prompt": P, "decode_steps": K, "max_seq": P + max(K, W)},
         "prefill_tok_s": round(P / prefill_s, 2),
         "sampled_decode_tok_s": round(K / sampled_s, 2),
-        "batched_decode": {"sequences": BB, "tok_s_aggregate": round(BB * K / (b_ms / 1e3), 1),
-                           "ms_per_step": round(b_ms / K, 3)},
+        "batched_decode": batched,
         "decode_bytes_per_token": int(bpt),
         "decode_hbm_frac": round(value * bpt / (HBM_PEAK_GBS * 1e9), 4),
         "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
