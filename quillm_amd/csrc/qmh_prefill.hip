@@ -453,16 +453,17 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 //
 // Up to BMV_P tokens (batched decode, short prompts): the decode matvec's organisation with one
 // record and one term per token. A workgroup owns a contiguous range of whole tiles (contiguous
-// slots: tile-major, then block, then row in tile). Its threads stream every slot once (BMV_U slots per
-// thread in flight, two register sets), and for each token form the block's exact int32 dot with
-// sdot4 against that token's activation record in LDS, then the term (float)acc * (dw * dx) into LDS
-// at [token][slot]. After the stream one lane per (row, token) walks its terms in block order from
-// +0 (the reference's chain) and runs the prefill epilogue (pf_store).
+// slots: tile-major, then block, then row in tile). Its threads stream every slot once (8 Q4_0 or 4
+// Q8_0 slots per thread per register set, two sets), and for each token form the block's exact int32
+// dot with sdot4 against that token's activation record in LDS, then the term (float)acc * (dw * dx)
+// into LDS at [token][slot]. After the stream one lane per (row, token) walks its terms in block order
+// from +0 (the reference's chain) and runs the prefill epilogue (pf_store).
 //
-// Records: 48 bytes per (block, token) built from the Q8_0 image of k_pf_quant, codes in the order
-// the weights pair with (Q8_0: element order; Q4_0: even elements, then odd: the image's perm8
+// Records: 48 bytes per (block, token), codes in the order the weights pair with (Q8_0: element
+// order; Q4_0: even elements, then odd), then d (fp32), then the code sum (Q4_0: sum (q - 8) x =
+// sum q x - 8 sum x, exact). They are built either from the Q8_0 image of k_pf_quant (its perm8
 // groups [e0 e2 e4 e6 e1 e3 e5 e7] give their first 4 bytes to the even half and the last 4 to the
-// odd half), then d (fp32), then the code sum (Q4_0: sum (q - 8) x = sum q x - 8 sum x, exact).
+// odd half) or, for a plain input, straight from the f32 rows (bmv_records_f32).
 #define BMV_P 4
 #define BMV_NT 512
 #define BMV_REC 48
