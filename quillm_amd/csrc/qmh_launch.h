@@ -110,6 +110,8 @@ typedef struct {
      * caches at out1/out2 + p*kv_stride; NULL / 0 for one prompt at positions pos0 + p */
     const int32_t *pos_arr;
     long long kv_stride;
+    /* set by the matmul launcher: the multi-token matvec's blocks per LDS round (0: all at once) */
+    int bmv_bq;
 } qmh_pf_args;
 int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tokens, int P, float *X,
                         void *stream);

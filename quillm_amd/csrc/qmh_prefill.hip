@@ -467,6 +467,7 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 #define BMV_P 4
 #define BMV_NT 512
 #define BMV_REC 48
+#define BMV_CH 4  // (row, token) pairs per thread: rows of a workgroup x tokens <= 4*BMV_NT
 #define BMV_LDS (160 * 1024)
 __host__ __device__ inline int bmv_ntiles(const qmh_pf_args &a) {
     return a.il ? a.rows_alloc / (a.tile_r / 2) : a.rows_alloc / a.tile_r;
@@ -526,7 +527,7 @@ __device__ __forceinline__ void bmv_records_f32(const qmh_pf_args &a, uint8_t *r
 }
 
 template <int WT>
-__global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
+__global__ __launch_bounds__(BMV_NT, 4) void k_bmv(qmh_pf_args a) {  // 4 waves per SIMD: two per CU
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;  // code bytes per slot
     constexpr int NV = CB / 16;
     constexpr int U = WT == QMH_Q8 ? 4 : 8;      // slots per thread per register set
@@ -536,21 +537,22 @@ __global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
     const int t0 = bmv_tile0(blockIdx.x, ntiles, gridDim.x), t1 = bmv_tile0(blockIdx.x + 1, ntiles, gridDim.x);
     const int ntw = t1 - t0;
     if (ntw <= 0) return;  // the host launches at most ntiles workgroups
-    const int TS = ntw * nb * R;  // slots of the range
+    // blocks per LDS round: all of them, or (one tile per workgroup) as many as let two workgroups
+    // share a CU; each round's terms extend the chains before the next round overwrites them
+    const int bq = a.bmv_bq > 0 && a.bmv_bq < nb && ntw == 1 ? a.bmv_bq : nb;
     float *T = (float *)(smem + (size_t)nb * P * BMV_REC);
     const uint8_t *cbase = a.codes + (size_t)t0 * nb * R * CB;
     const uint16_t *sbase = a.scales + (size_t)t0 * nb * R;
-
-    // slot l = j*BMV_NT + tid of the range: block column (l >> lgR) = (tid >> lgR) + j*(BMV_NT >> lgR);
-    // its block index is that mod nb, kept incrementally (step < nb)
-    const int nper = (TS + BMV_NT - 1) / BMV_NT;
-    const int bstep = (BMV_NT >> lgR) % nb;
     uint4 cA[U][NV], cB[U][NV];
     uint32_t sA[U], sB[U];
+    int q0 = 0, nbq = bq, TS = ntw * bq * R;  // the round's first block, blocks, slots
+    // slot l = j*BMV_NT + tid of the round: block column (l >> lgR) = (tid >> lgR) + j*(BMV_NT >> lgR);
+    // its block index in the round is that mod nbq, kept incrementally (step < nbq). With several
+    // tiles there is one round (q0 = 0); with rounds there is one tile, so slot q0*R + l of the range
     auto load = [&](uint4 (&c)[U][NV], uint32_t (&sc)[U], int j0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int l0 = (j0 + u) * BMV_NT + tid, l = l0 < TS ? l0 : TS - 1;
+            const int l0 = (j0 + u) * BMV_NT + tid, l = (l0 < TS ? l0 : TS - 1) + q0 * R;
 #pragma unroll
             for (int v = 0; v < NV; v++) c[u][v] = *(const uint4 *)(cbase + (size_t)l * CB + 16 * v);
             sc[u] = sbase[l];
@@ -589,87 +591,104 @@ __global__ __launch_bounds__(BMV_NT) void k_bmv(qmh_pf_args a) {
     }
     __syncthreads();
 
-    // the stream
-    int bcur = (tid >> lgR) % nb;
-    auto compute = [&](const uint4 (&c)[U][NV], const uint32_t (&sc)[U], int j0) {
+    // the rounds: stream (terms to LDS), then every chain extended over the round's blocks in order
+    const int rows_w = ntw * R, npair = rows_w * P;  // pair c = p*rows_w + i: row i of the range, token p
+    float yk[BMV_CH];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int l = (j0 + u) * BMV_NT + tid;
-            if (j0 + u < nper) {  // uniform
-                const float dw = qmh_h2f((uint16_t)sc[u]);
+    for (int kc = 0; kc < BMV_CH; kc++) yk[kc] = 0.0f;
+    for (q0 = 0; q0 < nb; q0 += bq) {
+        nbq = nb - q0 < bq ? nb - q0 : bq;
+        TS = ntw * nbq * R;
+        const int nper = (TS + BMV_NT - 1) / BMV_NT, bstep = (BMV_NT >> lgR) % nbq;
+        int bcur = (tid >> lgR) % nbq;
+        auto compute = [&](const uint4 (&c)[U][NV], const uint32_t (&sc)[U], int j0) {
 #pragma unroll
-                for (int p = 0; p < BMV_P; p++)
-                    if (p < P) {
-                        const uint8_t *rp = smem + (size_t)(bcur * P + p) * BMV_REC;
-                        const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);
-                        const float2 ds = *(const float2 *)(rp + 32);
-                        int acc;
-                        if (WT == QMH_Q4) {
-                            const uint4 w = c[u][0];
-                            acc = -8 * __float_as_int(ds.y);
-                            acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);
-                        } else {
-                            const uint4 w0 = c[u][0], w1 = c[u][NV - 1];
-                            acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, 0, false);
-                            acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);
-                            acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);
+            for (int u = 0; u < U; u++) {
+                const int l = (j0 + u) * BMV_NT + tid;
+                if (j0 + u < nper) {  // uniform
+                    const float dw = qmh_h2f((uint16_t)sc[u]);
+#pragma unroll
+                    for (int p = 0; p < BMV_P; p++)
+                        if (p < P) {
+                            const uint8_t *rp = smem + (size_t)((q0 + bcur) * P + p) * BMV_REC;
+                            const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);
+                            const float2 ds = *(const float2 *)(rp + 32);
+                            int acc;
+                            if (WT == QMH_Q4) {
+                                const uint4 w = c[u][0];
+                                acc = -8 * __float_as_int(ds.y);
+                                acc = __builtin_amdgcn_sdot4((int)(w.x & 0x0f0f0f0fu), x0.x, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0f0f0f0fu), x1.x, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)(w.y & 0x0f0f0f0fu), x0.y, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0f0f0f0fu), x1.y, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)(w.z & 0x0f0f0f0fu), x0.z, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0f0f0f0fu), x1.z, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)(w.w & 0x0f0f0f0fu), x0.w, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0f0f0f0fu), x1.w, acc, false);
+                            } else {
+                                const uint4 w0 = c[u][0], w1 = c[u][NV - 1];
+                                acc = __builtin_amdgcn_sdot4((int)w0.x, x0.x, 0, false);
+                                acc = __builtin_amdgcn_sdot4((int)w0.y, x0.y, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w0.z, x0.z, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w0.w, x0.w, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w1.x, x1.x, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w1.y, x1.y, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w1.z, x1.z, acc, false);
+                                acc = __builtin_amdgcn_sdot4((int)w1.w, x1.w, acc, false);
+                            }
+                            if (l < TS) T[(size_t)p * TS + l] = (float)acc * (dw * ds.x);
                         }
-                        if (l < TS) T[(size_t)p * TS + l] = (float)acc * (dw * ds.x);
-                    }
+                }
+                bcur += bstep;
+                bcur -= bcur >= nbq ? nbq : 0;
             }
-            bcur += bstep;
-            bcur -= bcur >= nb ? nb : 0;
+        };
+        if (q0 > 0) load(cA, sA, 0);  // the first round's set was issued before the records
+        for (int j0 = 0; j0 < nper; j0 += 2 * U) {
+            if (j0 + U < nper) load(cB, sB, j0 + U);
+            compute(cA, sA, j0);
+            if (j0 + 2 * U < nper) load(cA, sA, j0 + 2 * U);
+            if (j0 + U < nper) compute(cB, sB, j0 + U);
         }
-    };
-    for (int j0 = 0; j0 < nper; j0 += 2 * U) {
-        if (j0 + U < nper) load(cB, sB, j0 + U);
-        compute(cA, sA, j0);
-        if (j0 + 2 * U < nper) load(cA, sA, j0 + 2 * U);
-        if (j0 + U < nper) compute(cB, sB, j0 + U);
+        __syncthreads();
+#pragma unroll
+        for (int kc = 0; kc < BMV_CH; kc++) {
+            const int c = kc * BMV_NT + tid, p = c / rows_w, i = c - p * rows_w, tl = i >> lgR, r = i & (R - 1);
+            if (c < npair) {
+                const float *tp = T + (size_t)p * TS + (size_t)tl * nbq * R + r;
+                float y = yk[kc];
+                int b = 0;
+                for (; b + 16 <= nbq; b += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) v[k] = tp[(b + k) * R];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) y = y + v[k];
+                }
+                for (; b < nbq; b++) y = y + tp[b * R];
+                yk[kc] = y;
+            }
+        }
+        __syncthreads();  // the next round's terms overwrite these
     }
-    __syncthreads();
 
-    // chains and epilogues: pair c = p*rows_w + i (row i of the range: tile i >> lgR, row i & (R-1));
-    // a tile's rows are consecutive lanes of one wave (R divides 64, rows_w is a multiple of R)
-    const int rows_w = ntw * R, npair = rows_w * P;
-    for (int c0 = 0; c0 < npair; c0 += BMV_NT) {
-        const int c = c0 + tid, p = c / rows_w, i = c - p * rows_w, tl = i >> lgR, r = i & (R - 1);
-        float y = 0.0f;
-        if (c < npair) {
-            const float *tp = T + (size_t)p * TS + (size_t)tl * nb * R + r;
-            int b = 0;
-            for (; b + 16 <= nb; b += 16) {
-                float v[16];
+    // epilogues: a tile's rows are consecutive lanes of one wave (R divides 64, rows_w is a multiple of R)
 #pragma unroll
-                for (int k = 0; k < 16; k++) v[k] = tp[(b + k) * R];
-#pragma unroll
-                for (int k = 0; k < 16; k++) y = y + v[k];
+    for (int kc = 0; kc < BMV_CH; kc++)
+        if (kc * BMV_NT < npair) {  // uniform
+            const int c = kc * BMV_NT + tid, p = c / rows_w, i = c - p * rows_w, tl = i >> lgR, r = i & (R - 1);
+            const float y = yk[kc];
+            const int tile = t0 + tl;
+            if (a.il) {  // rows r < R/2 of a tile are W1 rows, r + R/2 their W3 rows
+                const float up = __shfl_down(y, R >> 1);
+                const int row = tile * (R >> 1) + r;
+                if (c < npair && r < (R >> 1) && row < a.rows) pf_store(a, row, p, y, up, 0.0f);
+            } else {
+                const float partner = __shfl_xor(y, 1);  // row ^ 1: RoPE's pair
+                const int row = tile * R + r;
+                if (c < npair && row < a.rows) pf_store(a, row, p, y, y, partner);
             }
-            for (; b < nb; b++) y = y + tp[b * R];
         }
-        const int tile = t0 + tl;
-        if (a.il) {  // rows r < R/2 of a tile are W1 rows, r + R/2 their W3 rows
-            const float up = __shfl_down(y, R >> 1);
-            const int row = tile * (R >> 1) + r;
-            if (c < npair && r < (R >> 1) && row < a.rows) pf_store(a, row, p, y, up, 0.0f);
-        } else {
-            const float partner = __shfl_xor(y, 1);  // row ^ 1: RoPE's pair
-            const int row = tile * R + r;
-            if (c < npair && row < a.rows) pf_store(a, row, p, y, y, partner);
-        }
-    }
 }
 
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
@@ -688,7 +707,8 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     // k_pf_quant's launch, while an RMSNorm'd input quantized in every workgroup was 6 us slower.
     const int ntiles = bmv_ntiles(*a);
     const size_t rec = (size_t)a->nb * a->P * BMV_REC, per_tile = (size_t)a->P * a->tile_r * a->nb * sizeof(float);
-    const bool bmv = a->P <= BMV_P && rec + per_tile <= BMV_LDS;
+    const bool bmv = a->P <= BMV_P && rec + per_tile <= BMV_LDS &&
+                     (size_t)a->tile_r * a->P * ((ntiles + 255) / 256) <= (size_t)BMV_CH * BMV_NT;
     const bool fuse = bmv && a->xf && !a->norm_w;
     if (a->xf && !fuse) {  // the quantized image first
         const int rc = qmh_launch_pf_quant(a->xf, a->ldxf, a->norm_w, a->eps, a->nxf, a->P, (int8_t *)a->xc,
@@ -701,7 +721,18 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
         // whole tiles per workgroup: about one workgroup per CU (256), fewer tiles if LDS asks
         const int fit = (int)((BMV_LDS - rec) / per_tile), want = ntiles / 256 > 1 ? ntiles / 256 : 1;
         const int k = want < fit ? want : fit, G = (ntiles + k - 1) / k;
-        const size_t lds = rec + (size_t)((ntiles + G - 1) / G) * per_tile;
+        size_t lds = rec + (size_t)((ntiles + G - 1) / G) * per_tile;
+        // one tile per workgroup, more workgroups than CUs and room for one per CU: LDS rounds of bq
+        // blocks so that two share a CU
+        b.bmv_bq = 0;
+        const size_t per_block = (size_t)a->P * a->tile_r * sizeof(float);
+        if (k == 1 && ntiles > 256 && 2 * lds > BMV_LDS && 2 * rec < BMV_LDS) {
+            const int bq = (int)((BMV_LDS / 2 - rec) / per_block);
+            if (bq >= 16 && bq < a->nb) {
+                b.bmv_bq = bq;
+                lds = rec + (size_t)bq * per_block;
+            }
+        }
         if (a->dtype == QMH_Q4) hipLaunchKernelGGL(k_bmv<QMH_Q4>, dim3(G), dim3(BMV_NT), lds, s, b);
         else hipLaunchKernelGGL(k_bmv<QMH_Q8>, dim3(G), dim3(BMV_NT), lds, s, b);
         return (int)hipGetLastError();
