@@ -119,6 +119,11 @@ qmh_model *qmh_model_create(const qmh_config *cfg, const qmh_tensor_view *tok_em
 qmh_model *qmh_model_load(const char *path, int32_t max_seq);
 void qmh_model_free(qmh_model *m);
 const qmh_config *qmh_model_config(const qmh_model *m);
+/* The configuration a .qlm file gives the model, read and validated as qm_model_load does
+ * before it touches tensors (src/model.c:35-53: the seven u32 keys, rope_theta / norm_eps with
+ * their defaults, the head checks, the max_seq cap; the first entry of a duplicated key wins, as
+ * qlm_find_kv's does, src/qlm_file.c:181-185). Needs no device. 0, or -1 with a message. */
+int qmh_qlm_config(const char *path, int32_t max_seq, qmh_config *out);
 
 /* One token at position pos; returns model-owned logits[vocab] in pinned host memory, or
  * NULL for token outside [0, vocab) or pos outside [0, max_seq). qm_model_forward
@@ -143,7 +148,7 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
  * the reference decodes one sequence, src/model.c:158-191). Each sequence has its own KV cache of
  * the model's max_seq positions, separate from the model's own. Per sequence, logits and KV contents
  * are bitwise those of the single-sequence qmh_model_forward at the same tokens and positions.
- * Needs quantized weights and head_dim <= 128; n_seq in [1, min(max_seq, 512)]. NULL on error. */
+ * Needs quantized weights and head_dim <= 128, a multiple of 4; n_seq in [1, min(max_seq, 512)]. NULL on error. */
 typedef struct qmh_batch qmh_batch;
 qmh_batch *qmh_batch_create(qmh_model *m, int32_t n_seq);
 void qmh_batch_free(qmh_batch *b);
@@ -177,7 +182,9 @@ int32_t qmh_sample_sync(qmh_sampler *s, const float *logits);
 /* The rng state (qm_sampler.rng) after the library stream's work. */
 int qmh_sampler_rng(const qmh_sampler *s, uint64_t *state);
 /* Diagnostics of the last non-greedy draw (no reference counterpart): diag[0] the serial double
- * sum of the exponentials, [1] 0 when every chunk replay agreed, [2] chunks replayed serially
+ * sum of the exponentials, [1] 0 when every chunk certificate held, else nonzero: the sums were
+ * then recomputed by one serial pass (as they are for every draw of a sampler created while the
+ * environment variable QMH_SAMPLER_SERIAL is set), so the token stays exact, [2] chunks replayed serially
  * for that sum, [3] candidates, [4] k, [5] nucleus size m, [6] chunks replayed for the nucleus
  * sum, [7] nucleus mass. probs (NULL or host [n_vocab]): the normalised probabilities. */
 int qmh_sampler_diag(const qmh_sampler *s, double diag[8], float *probs);

@@ -87,6 +87,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_model_load": (vp, [ctypes.c_char_p, i32]),
         "qmh_model_free": (None, [vp]),
         "qmh_model_config": (ctypes.POINTER(QmhConfig), [vp]),
+        "qmh_qlm_config": (ctypes.c_int, [ctypes.c_char_p, i32, ctypes.POINTER(QmhConfig)]),
         "qmh_model_forward": (ctypes.POINTER(ctypes.c_float), [vp, i32, i32]),
         "qmh_model_prefill": (ctypes.c_int, [vp, vp, i32, i32, vp]),
         "qmh_model_greedy": (ctypes.c_int, [vp, i32, i32, i32, vp]),
@@ -130,6 +131,13 @@ def last_error() -> str:
 def _check(rc: int, what: str):
     if rc != 0:
         raise QmhError(f"{what}: {last_error()}")
+
+
+def qlm_config(path: str, max_seq: int = 0) -> "QmhConfig":
+    """The configuration a .qlm file gives the model (qmh_qlm_config; no device needed)."""
+    c = QmhConfig()
+    _check(load_library().qmh_qlm_config(path.encode(), int(max_seq), ctypes.byref(c)), "qlm_config")
+    return c
 
 
 def available() -> bool:

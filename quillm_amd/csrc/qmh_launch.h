@@ -162,6 +162,7 @@ typedef struct {
     int record_cap;
     double *diag;
     void *ws; /* qmh_sample_ws_bytes(n) bytes, zeroed once at allocation (large vocabularies) */
+    int force_serial; /* nonzero: both exact sums take the serial pass that a failed certificate takes */
 } qmh_sample_args;
 size_t qmh_sample_ws_bytes(int n);
 int qmh_launch_sample(const qmh_sample_args *a, void *stream);

@@ -425,9 +425,11 @@ __device__ void block_xfer_exscan(long long &c0, long long &c1, int &co, long lo
 // From the chunk classes and transfers in x: the segmented scan, the serial walk over replayed
 // chunks, every chunk's exact start / end and the total. A certified chunk whose transfer leaves its
 // binade, or a chunk end that is not the next chunk's start, sets `bad` in x.status (never
-// expected). Block-wide call.
+// expected); the starts, ends and total are then recomputed by one serial pass in the reference's
+// order, so the result stays exact. force: take that serial pass unconditionally (a host switch
+// that lets tests run it). Block-wide call.
 template <int NT, class Get>
-__device__ void finish_sums(const Get &get, int len, int ch, int nch, ExSums &x, int bad) {
+__device__ void finish_sums(const Get &get, int len, int ch, int nch, ExSums &x, int bad, bool force) {
     const int t = threadIdx.x, lane = t & 63;
     {
         // thread t composes chunks [t*per, t*per+per), then one scan over the threads
@@ -499,10 +501,24 @@ __device__ void finish_sums(const Get &get, int len, int ch, int nch, ExSums &x,
     for (int c = t; c + 1 < nch; c += NT)
         if (x.end[c] != x.start[c + 1]) atomicOr(&x.status, bad);
     if (t == 0) {
+        if (force) x.status |= bad;
         x.total = nch > 0 ? x.end[nch - 1] : 0.0;
         x.nch = nch;
     }
     __syncthreads();
+    if (x.status & bad) {  // uniform: the serial sum s += v over every element, chunk by chunk
+        if (t < 64) {
+            double s = 0.0;
+            for (int c = 0; c < nch; c++) {
+                if (lane == 0) x.start[c] = s;
+                int dummy;
+                s = wave_replay(get, c * ch, min(c * ch + ch, len), s, [](double) { return false; }, &dummy);
+                if (lane == 0) x.end[c] = s;
+            }
+            if (lane == 0) x.total = nch > 0 ? s : 0.0;
+        }
+        __syncthreads();
+    }
 }
 
 // chunk geometry of an exact sum over len elements
@@ -658,7 +674,7 @@ __global__ __launch_bounds__(NT1) void k_sample(qmh_sample_args a) {
             }
         }
         __syncthreads();
-        finish_sums<NT1>(getp, n, ch, nch, x, 1);
+        finish_sums<NT1>(getp, n, ch, nch, x, 1, a.force_serial != 0);
     }
     const double S = x.total;
     const int nx_sum = x.nx;
@@ -793,7 +809,7 @@ __global__ __launch_bounds__(NT1) void k_sample(qmh_sample_args a) {
         }
     }
     __syncthreads();
-    finish_sums<NT1>(getq, kk, ch2, nch2, x, 2);
+    finish_sums<NT1>(getq, kk, ch2, nch2, x, 2, a.force_serial != 0);
     const int nx_nuc = x.nx;
     const double tp = (double)a.top_p;
     const int first = exact_first<NT1>(getq, ch2, kk, x, [&](double s) { return s >= tp; });
@@ -973,7 +989,7 @@ __global__ __launch_bounds__(GT) void k_smp_xfer(qmh_sample_args a) {
 
 // the chunk classes and transfers into LDS, then the exact sum (one 1024-thread workgroup)
 template <class Get>
-__device__ void fin_sums(const Get &get, int len, const Ws &ws, ExSums &x, int bad) {
+__device__ void fin_sums(const Get &get, int len, const Ws &ws, ExSums &x, int bad, bool force) {
     const int t = threadIdx.x;
     const int J = chunk_j(len), ch = 64 * J, nch = (len + ch - 1) / ch;
     if (t == 0) x.status = 0;
@@ -984,7 +1000,7 @@ __device__ void fin_sums(const Get &get, int len, const Ws &ws, ExSums &x, int b
         x.fo[k] = ws.fo[k];
     }
     __syncthreads();
-    finish_sums<NTF>(get, len, ch, nch, x, bad);
+    finish_sums<NTF>(get, len, ch, nch, x, bad, force);
 }
 
 // K3: the exact normaliser
@@ -993,7 +1009,7 @@ __global__ __launch_bounds__(NTF) void k_smp_norm(qmh_sample_args a) {
     const Ws ws = ws_of(a);
     if (ws.ctl->nan) return;
     const float *pv = a.p;
-    fin_sums([&](int i) { return pv[i]; }, a.n, ws, x, 1);
+    fin_sums([&](int i) { return pv[i]; }, a.n, ws, x, 1, a.force_serial != 0);
     if (threadIdx.x == 0) {
         ws.ctl->S = x.total;
         ws.ctl->nx_sum = x.nx;
@@ -1239,7 +1255,7 @@ __global__ __launch_bounds__(NTF) void k_smp_draw(qmh_sample_args a) {
     const int kk = ctl->kk;
     const uint32_t *kv = sorted_keys(a, ctl);
     auto getq = [&](int i) { return key_prob(kv[i]); };
-    fin_sums(getq, kk, ws, x, 2);
+    fin_sums(getq, kk, ws, x, 2, a.force_serial != 0);
     const int ch = 64 * chunk_j(kk);
     const double tp = (double)a.top_p;
     const int first = exact_first<NTF>(getq, ch, kk, x, [&](double s) { return s >= tp; });

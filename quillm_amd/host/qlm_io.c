@@ -94,6 +94,7 @@ int qlm_map_open(qlm_map *f, const char *path, char *err, size_t errlen) {
     static const char *keys[7] = {"llama.dim",        "llama.hidden_dim", "llama.n_layers", "llama.n_heads",
                                   "llama.n_kv_heads", "llama.vocab_size", "llama.max_seq"};
     int32_t *dst[7] = {&c->dim, &c->hidden_dim, &c->n_layers, &c->n_heads, &c->n_kv_heads, &c->vocab_size, &c->max_seq};
+    int seen[9] = {0}; /* the 7 keys above, rope_theta, norm_eps */
     for (uint32_t i = 0; i < n_kv; i++) {
         char key[64];
         if (rd_name(&r, key, sizeof key)) goto bad;
@@ -106,13 +107,22 @@ int qlm_map_open(qlm_map *f, const char *path, char *err, size_t errlen) {
             rd_take(&r, (size_t)cnt * 4);
         } else goto bad;
         if (r.bad) goto bad;
+        /* the first entry of a key decides, as the reference's lookup returns the first match
+         * (src/qlm_file.c:181-185; src/model.c:8-21): a later duplicate is ignored */
         for (int k = 0; k < 7; k++)
-            if (!strcmp(key, keys[k])) {
+            if (!seen[k] && !strcmp(key, keys[k])) {
+                seen[k] = 1;
                 f->have[k] = ty == 0 && v != 0 && v <= (1u << 24);
                 if (f->have[k]) *dst[k] = (int32_t)v;
             }
-        if (ty == 1 && !strcmp(key, "llama.rope_theta")) memcpy(&c->rope_theta, &v, 4);
-        if (ty == 1 && !strcmp(key, "llama.norm_eps")) memcpy(&c->norm_eps, &v, 4);
+        if (!seen[7] && !strcmp(key, "llama.rope_theta")) {
+            seen[7] = 1;
+            if (ty == 1) memcpy(&c->rope_theta, &v, 4);
+        }
+        if (!seen[8] && !strcmp(key, "llama.norm_eps")) {
+            seen[8] = 1;
+            if (ty == 1) memcpy(&c->norm_eps, &v, 4);
+        }
     }
     f->tensors = calloc(n_t ? n_t : 1, sizeof(qlm_tensor));
     if (!f->tensors) goto bad;

@@ -713,7 +713,9 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipHostMalloc((void **)&m->h_tokpos, sizeof(int32_t) * 4 * (size_t)S_, hipHostMallocDefault));
     HIPCHK(hipHostMalloc((void **)&m->h_logits, sizeof(float) * V, hipHostMallocDefault));
     /* batched prefill buffers (models whose matrices are all quantized) */
-    m->pf_ok = m->output.dtype != QMH_F32 && m->hd <= 256;
+    /* the batched prompt path's attention (k_pf_*, k_bt_*) takes head_dim <= 128 in whole float4s;
+     * other models run the prompt as sequential forwards */
+    m->pf_ok = m->output.dtype != QMH_F32 && m->hd <= 128 && m->hd % 4 == 0;
     for (int l = 0; l < c->n_layers && m->pf_ok; l++) {
         const dev_layer *L = &m->layers[l];
         m->pf_ok = L->qkv.dtype != QMH_F32 && L->wo.dtype != QMH_F32 && L->w13.dtype != QMH_F32 &&
@@ -814,6 +816,25 @@ done:
 }
 
 const qmh_config *qmh_model_config(const qmh_model *m) { return m ? &m->cfg : NULL; }
+
+int qmh_qlm_config(const char *path, int32_t max_seq, qmh_config *out) {
+    if (!path || !out) return fail("qlm_config: NULL argument");
+    qlm_map f;
+    char err[256];
+    if (qlm_map_open(&f, path, err, sizeof err)) return fail("%s", err);
+    static const char *keys[7] = {"llama.dim",        "llama.hidden_dim", "llama.n_layers", "llama.n_heads",
+                                  "llama.n_kv_heads", "llama.vocab_size", "llama.max_seq"};
+    qmh_config c = f.cfg;
+    int rc = 0;
+    for (int k = 0; k < 7 && rc == 0; k++)
+        if (!f.have[k]) rc = fail("missing/invalid metadata '%s'", keys[k]); /* src/model.c:8-16 */
+    if (rc == 0 && (c.dim % c.n_heads || c.n_heads % c.n_kv_heads || (c.dim / c.n_heads) % 2 || c.n_layers > 1024))
+        rc = fail("inconsistent head configuration"); /* src/model.c:48-52 */
+    if (rc == 0 && max_seq > 0 && max_seq < c.max_seq) c.max_seq = max_seq; /* src/model.c:53 */
+    qlm_map_close(&f);
+    if (rc == 0) *out = c;
+    return rc;
+}
 
 float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
     if (!m || token < 0 || token >= m->cfg.vocab_size || pos < 0 || pos >= m->cfg.max_seq) return NULL;
@@ -1032,11 +1053,11 @@ qmh_batch *qmh_batch_create(qmh_model *m, int32_t n_seq) {
         return NULL;
     }
     if (!m->pf_ok) {
-        fail("batch: needs quantized weights and head_dim <= 128 (the batched matmul path)");
+        fail("batch: needs quantized weights and head_dim <= 128, a multiple of 4 (the batched matmul path)");
         return NULL;
     }
-    if (n_seq < 1 || n_seq > m->pf_cap || m->hd > 128) {
-        fail("batch: n_seq %d outside [1, %d] or head_dim %d > 128", (int)n_seq, m->pf_cap, m->hd);
+    if (n_seq < 1 || n_seq > m->pf_cap) {
+        fail("batch: n_seq %d outside [1, %d]", (int)n_seq, m->pf_cap);
         return NULL;
     }
     qmh_batch *b = calloc(1, sizeof *b);
@@ -1175,6 +1196,7 @@ struct qmh_sampler {
     uint32_t *d_key[2];
     int32_t *d_idx[2];
     void *d_ws; /* control block and chunk arrays of the multi-workgroup path */
+    int force_serial; /* QMH_SAMPLER_SERIAL set at creation: every exact sum by the serial fallback */
 };
 
 /* the reference's greedy shortcut (src/sampler.c:52): no draw, the rng is left alone */
@@ -1206,6 +1228,7 @@ qmh_sampler *qmh_sampler_create(int32_t n_vocab, float temperature, int top_k, f
     s->top_k = top_k < 0 ? 0 : top_k;
     s->top_p = (top_p <= 0 || top_p > 1) ? 1.0f : top_p;
     uint64_t rng = seed ? seed : 0x9e3779b97f4a7c15ULL;
+    s->force_serial = getenv("QMH_SAMPLER_SERIAL") != NULL;
     const size_t n = (size_t)n_vocab;
     hipError_t e = hipMalloc((void **)&s->d_rng, sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc((void **)&s->d_diag, 8 * sizeof(double));
@@ -1244,6 +1267,7 @@ static qmh_sample_args sample_args(const qmh_sampler *s, const float *logits) {
     a.idx1 = s->d_idx[1];
     a.diag = s->d_diag;
     a.ws = s->d_ws;
+    a.force_serial = s->force_serial;
     return a;
 }
 

@@ -249,6 +249,9 @@ class Ref:
             "qm_sampler_init": (ctypes.c_int, [vp, vp, i32, f32, ctypes.c_int, f32, ctypes.c_uint64]),
             "qm_sample": (i32, [vp, vp]),
             "qm_rng_uniform": (f32, [vp]),
+            "qm_model_load": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
+                                             ctypes.c_size_t]),
+            "qm_model_free": (None, [vp]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -277,6 +280,21 @@ class Ref:
         for r in range(rows):
             fn(_ptr(x[r]), out[r].ctypes.data, n)
         return out
+
+    def model_config(self, path: str, max_seq: int = 0):
+        """(config dict, None) from the reference's own qm_model_load (src/model.c:35-117), or
+        (None, its error message). qm_config is the first member of qm_model (src/model.h:17-18)."""
+        m = ctypes.create_string_buffer(1 << 16)  # larger than sizeof(qm_model)
+        err = ctypes.create_string_buffer(256)
+        if self.L.qm_model_load(m, path.encode(), 1, max_seq, err, 256) != 0:
+            return None, err.value.decode()
+        v = np.frombuffer(m.raw[:36], dtype=np.int32)
+        f = np.frombuffer(m.raw[28:36], dtype=np.float32)
+        cfg = dict(zip(("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size", "max_seq"),
+                       (int(x) for x in v[:7])))
+        cfg["rope_theta"], cfg["norm_eps"] = float(f[0]), float(f[1])
+        self.L.qm_model_free(m)
+        return cfg, None
 
     def matvec(self, dtype, W, rows, cols, x):
         t = QmTensor(b"w", dtype, 2, (ctypes.c_int64 * 4)(rows, cols, 0, 0), W.ctypes.data)

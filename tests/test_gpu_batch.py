@@ -160,16 +160,17 @@ def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positio
         assert np.array_equal(bits(outs[0][b]), bits(want)), f"sequence {b} (pos {pos[b]})"
 
 
-def test_batch_forward_wide_q4(gpu, oracle, tmp_path):
+@pytest.mark.parametrize("wt", ["q4_0", "q8_0"])
+def test_batch_forward_wide(gpu, oracle, tmp_path, wt):
     """The 7B layer shapes (4096 wide, hidden 11008, one layer, vocabulary 8192): the multi-token matvec
     gives each workgroup 2-3 tiles of QKV, Wo, W2 and the output, and runs W1|W3 (344 tiles) in LDS
-    rounds at 3 and 4 tokens. Per-sequence logits at 2, 3 and 4 sequences, mixed positions, bitwise the
-    oracle's single-sequence forwards."""
-    say("batch wide q4_0")
+    rounds at 3 and 4 tokens, for both weight types (their slot widths differ). Per-sequence logits at
+    2, 3 and 4 sequences, mixed positions, bitwise the oracle's single-sequence forwards."""
+    say("batch wide", wt)
     cfg = gpu.QmhConfig(dim=4096, hidden_dim=11008, n_layers=1, n_heads=32, n_kv_heads=32, vocab_size=8192,
                         max_seq=16, rope_theta=10000.0, norm_eps=1e-5)
-    path = str(tmp_path / "wide_q4_0.qlm")
-    gpu.gen_model(path, cfg, "q4_0", seed=5, threads=8)
+    path = str(tmp_path / f"wide_{wt}.qlm")
+    gpu.gen_model(path, cfg, wt, seed=5, threads=8)
     rs = np.random.default_rng(3)
     with gpu.Model.load(path) as m:
         V = m.vocab

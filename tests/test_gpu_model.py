@@ -153,3 +153,35 @@ def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
             os.environ.pop("QMH_PREFILL_SEQ", None)
     for got, want in zip(runs[0], runs[1]):
         assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("name,dims,wt,spans", [
+    # one query head per kv head, head_dim 128: decode attention past one 640-position chunk
+    # (positions 638-642 cross into the second chunk, 1279-1281 into the third)
+    ("mha128", dict(dim=256, hidden_dim=320, n_layers=1, n_heads=2, n_kv_heads=2, vocab_size=300, max_seq=1300),
+     "q4_0", [(636, 646), (1277, 1286)]),
+    # head_dim 10 (not a multiple of 4): the scalar-column decode attention, and prompts that run as
+    # sequential forwards (the batched prompt path takes head_dim % 4 == 0 only)
+    ("mha10", dict(dim=60, hidden_dim=128, n_layers=1, n_heads=6, n_kv_heads=6, vocab_size=300, max_seq=700),
+     "q8_0", [(636, 646), (690, 700)]),
+])
+def test_long_context_decode_matches_oracle(gpu, oracle, tmp_path, name, dims, wt, spans):
+    """Decode forwards at positions on either side of the attention kernels' chunk boundaries
+    (src/model.c:132-156 attends over every pos < max_seq), the positions between them filled by
+    prefill: logits bitwise the oracle's at every position."""
+    path = str(tmp_path / f"{name}.qlm")
+    gpu.gen_model(path, gpu.QmhConfig(**dims, rope_theta=10000.0, norm_eps=1e-5), wt, seed=41, threads=4)
+    n = spans[-1][1]
+    toks = gpu.prompt_ids(n, dims["vocab_size"], seed=17)
+    say(f"case {name}: oracle over {n} positions")
+    want, _ = oracle.run_model(path, toks, n_gen=0)
+    with gpu.Model.load(path) as m:
+        p = 0
+        for lo, hi in spans:
+            say(f"case {name}: prefill {p}..{lo - 1}, forwards {lo}..{hi - 1}")
+            lg = m.prefill(toks[p:lo], p, want_logits=True)
+            assert np.array_equal(bits(lg), bits(want[p:lo])), f"prefill positions {p}..{lo - 1}"
+            for i in range(lo, hi):
+                got = m.forward(int(toks[i]), i)
+                assert np.array_equal(bits(got), bits(want[i])), f"position {i}: max |d| {np.abs(got - want[i]).max()}"
+            p = hi

@@ -30,7 +30,7 @@ def bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
-def check_seq(gpu, oracle, ref, n, cfg, seed, seq, check_probs=True):
+def check_seq(gpu, oracle, ref, n, cfg, seed, seq, check_probs=True, forced=False):
     dev = gpu.Sampler(n, *cfg, seed)
     rs = RefSampler(ref, n, *cfg, seed)
     orc = oracle.sampler(n, *cfg, seed)
@@ -44,7 +44,10 @@ def check_seq(gpu, oracle, ref, n, cfg, seed, seq, check_probs=True):
             if greedy:
                 continue
             d, q = dev.diag(probs=check_probs)
-            assert d[1] == 0, f"chunk replay mismatch (status {d[1]})"
+            if forced:  # every exact sum took the serial pass
+                assert d[1] != 0 or np.isnan(d[0]), "forced serial pass not reported"
+            else:
+                assert d[1] == 0, f"chunk replay mismatch (status {d[1]})"
             orc.sample(lg)
             if np.isnan(orc.total.value):
                 continue
@@ -80,6 +83,19 @@ def test_sampler_grid_path_sizes(gpu, oracle, ref, n):
         rs = np.random.default_rng(zlib.crc32(repr((n, cfg)).encode()))
         seq = [logit_family(k, n, rs) for k in ("normal2", "peaky", "flat", "ties", "wide", "zeros")]
         check_seq(gpu, oracle, ref, n, cfg, 23, seq)
+
+
+@pytest.mark.parametrize("n", [5000, 32000])
+def test_sampler_serial_fallback(gpu, oracle, ref, monkeypatch, n):
+    """The path a failed binade certificate takes (recomputing every chunk start and end by one
+    serial pass), forced from the host for a sampler created with QMH_SAMPLER_SERIAL set: tokens and
+    rng states stay the reference's, on both the one-workgroup (n <= 8192) and the grid path."""
+    say("sampler serial fallback", n)
+    monkeypatch.setenv("QMH_SAMPLER_SERIAL", "1")
+    rs = np.random.default_rng(zlib.crc32(repr(("fallback", n)).encode()))
+    seq = [logit_family(k, n, rs) for k in ("normal2", "peaky", "flat", "ties", "wide")]
+    for cfg in [(0.8, 0, 0.95), (1.0, 0, 1.0), (0.7, 40, 0.9)]:
+        check_seq(gpu, oracle, ref, n, cfg, 31, seq, forced=True)
 
 
 def test_sampler_large_vocab(gpu, oracle, ref):
