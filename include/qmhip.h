@@ -189,6 +189,17 @@ int qmh_sampler_rng(const qmh_sampler *s, uint64_t *state);
  * sum, [7] nucleus mass. probs (NULL or host [n_vocab]): the normalised probabilities. */
 int qmh_sampler_diag(const qmh_sampler *s, double diag[8], float *probs);
 
+/* qmh_sample without a sampler object, allocating nothing: no counterpart in the reference. It is
+ * for callers that cannot allocate device memory (code under HIP graph capture, serving loops).
+ * Same draw as qm_sample (src/sampler.c:50-106) with a sampler of these parameters, normalised as
+ * qm_sampler_init does; *rng (device memory) holds the xorshift64* state and is advanced in place,
+ * *out (device) receives the token, asynchronously on the stream (NULL = the library's). Scratch:
+ * one static device array of 3186944 bytes per GPU, held until the process ends, so n_vocab is at
+ * most 131072 (-1 otherwise). Calls that overlap on one GPU race on that array. qmh_init must have
+ * run. 0 or -1. */
+int qmh_sample_noalloc(const float *logits, int32_t n_vocab, float temperature, int top_k, float top_p,
+                       uint64_t *rng, int32_t *out, void *stream);
+
 /* Sampled decode on the device: n_steps forwards starting with token at pos, each next token
  * qm_sample of the previous logits (the generation loop of src/main.c:131-141). out[k] receives
  * the token sampled from the logits at position pos+k. No host round trip between steps. EOS does

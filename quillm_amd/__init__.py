@@ -99,6 +99,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_sampler_free": (None, [vp]),
         "qmh_sample": (ctypes.c_int, [vp, vp, vp, vp]),
         "qmh_sample_sync": (i32, [vp, vp]),
+        "qmh_sample_noalloc": (ctypes.c_int, [vp, i32, f32, ctypes.c_int, f32, vp, vp, vp]),
         "qmh_sampler_rng": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64)]),
         "qmh_sampler_diag": (ctypes.c_int, [vp, vp, vp]),
         "qmh_model_sample": (ctypes.c_int, [vp, vp, i32, i32, i32, vp]),

@@ -166,6 +166,14 @@ typedef struct {
 } qmh_sample_args;
 size_t qmh_sample_ws_bytes(int n);
 int qmh_launch_sample(const qmh_sample_args *a, void *stream);
+/* The sampler's static scratch (qmh_sample.hip): a file-scope device array of QMH_SAMPLE_NOALLOC_BYTES
+ * holding p, key0/1, idx0/1 and the grid workspace for up to QMH_SAMPLE_NOALLOC_MAX_VOCAB entries.
+ * qmh_sample_scratch: its device address on the current device (looked up once per device).
+ * qmh_launch_sample_scratch: points a's buffers into it (base = that address) and launches the draw. */
+#define QMH_SAMPLE_NOALLOC_MAX_VOCAB 131072
+#define QMH_SAMPLE_NOALLOC_BYTES 3186944
+int qmh_sample_scratch(void **ptr);
+int qmh_launch_sample_scratch(qmh_sample_args *a, void *base, void *stream);
 
 /* gate = silu(gate)*up over n (src/ops.c:128-133) */
 int qmh_launch_swiglu(float *gate, const float *up, int64_t n, void *stream);

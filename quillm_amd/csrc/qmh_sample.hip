@@ -36,6 +36,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "qmh_device.h"
 #include "qmh_launch.h"
 
@@ -857,9 +859,9 @@ struct Ws {
     uint32_t *hist;  // [4][ntile_max * 256]
 };
 
-__host__ __device__ inline size_t ws_align(size_t b) { return (b + 255) & ~(size_t)255; }
-__host__ __device__ inline int ntile_max(int n) { return (n + TILE - 1) / TILE; }
-__host__ __device__ inline size_t ws_bytes(int n) {
+__host__ __device__ constexpr size_t ws_align(size_t b) { return (b + 255) & ~(size_t)255; }
+__host__ __device__ constexpr int ntile_max(int n) { return (n + TILE - 1) / TILE; }
+__host__ __device__ constexpr size_t ws_bytes(int n) {
     return ws_align(sizeof(Ctl)) + ws_align(MAXCH * 8) * 3 + ws_align(4 * GMAX * 4) + ws_align(MAXCH * 4) * 3 +
            ws_align((size_t)4 * ntile_max(n) * 256 * 4);
 }
@@ -1285,7 +1287,65 @@ __global__ __launch_bounds__(NTF) void k_smp_draw(qmh_sample_args a) {
     }
 }
 
+// zeroes the control block of a workspace whose previous contents are unknown (the static scratch)
+__global__ void k_smp_clear(qmh_sample_args a) {
+    uint32_t *c = (uint32_t *)a.ws;
+    for (int i = threadIdx.x; i < (int)(sizeof(Ctl) / 4); i += blockDim.x) c[i] = 0;
+}
+
+// ---------------------------------------------------------------- static scratch
+//
+// The scratch of qmh_sample_noalloc: the probabilities, the two key and two index buffers of the
+// radix sort, and the grid path's workspace, for vocabularies up to QMH_SAMPLE_NOALLOC_MAX_VOCAB.
+// One copy per GPU, held until the process ends; every call on a GPU shares it.
+constexpr size_t SCR_N = QMH_SAMPLE_NOALLOC_MAX_VOCAB;
+constexpr size_t SCR_ARR = ws_align(SCR_N * 4);  // one [n] array of 4-byte elements
+constexpr size_t SCR_BYTES = 5 * SCR_ARR + ws_align(ws_bytes((int)SCR_N));
+static_assert(SCR_BYTES == QMH_SAMPLE_NOALLOC_BYTES, "scratch size stated in qmh_launch.h");
+
 }  // namespace
+
+static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
+
+// device address of the scratch on each device, looked up once per device with it current
+#define QMH_MAX_DEVICES 64
+static void *g_scratch_ptr[QMH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+extern "C" int qmh_sample_scratch(void **ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= QMH_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return 0;
+}
+
+// the buffers of qmh_sample_args inside the scratch at base (a device address); the grid path's
+// control block is cleared by a fill kernel on the stream first
+extern "C" int qmh_launch_sample_scratch(qmh_sample_args *a, void *base, void *stream) {
+    if (a->n < 1 || (size_t)a->n > SCR_N) return (int)hipErrorInvalidValue;
+    uint8_t *b = (uint8_t *)base;
+    a->p = (float *)b;
+    a->key0 = (uint32_t *)(b + SCR_ARR);
+    a->key1 = (uint32_t *)(b + 2 * SCR_ARR);
+    a->idx0 = (int32_t *)(b + 3 * SCR_ARR);
+    a->idx1 = (int32_t *)(b + 4 * SCR_ARR);
+    a->ws = b + 5 * SCR_ARR;
+    if (a->n > SMALL_N) {
+        hipLaunchKernelGGL(k_smp_clear, dim3(1), dim3(64), 0, (hipStream_t)stream, *a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+    }
+    return qmh_launch_sample(a, stream);
+}
 
 extern "C" size_t qmh_sample_ws_bytes(int n) { return n > SMALL_N ? ws_bytes(n) : 0; }
 

@@ -77,6 +77,8 @@ int qmh_init(int device) {
     HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     HIPCHK(hipMalloc((void **)&g_rope_scratch, sizeof(float) * 2 * ROPE_SCRATCH_PAIRS));
     g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    void *scr = NULL; /* the sampler's static scratch: its address on this device, looked up now */
+    LCHK(qmh_sample_scratch(&scr));
     g_dev = device;
     g_ready = 1;
     return 0;
@@ -1281,6 +1283,35 @@ int qmh_sample(qmh_sampler *s, const float *logits, int32_t *out, void *stream) 
     qmh_sample_args a = sample_args(s, logits);
     a.out = out;
     LCHK(qmh_launch_sample(&a, S(stream)));
+    return 0;
+}
+
+int qmh_sample_noalloc(const float *logits, int32_t n_vocab, float temperature, int top_k, float top_p,
+                       uint64_t *rng, int32_t *out, void *stream) {
+    /* no implicit qmh_init here: it allocates (the library stream, a rope table) */
+    if (!g_ready) return fail("sample_noalloc: call qmh_init first");
+    if (!logits || !rng || !out) return fail("sample_noalloc: NULL argument");
+    if (n_vocab < 1 || n_vocab > QMH_SAMPLE_NOALLOC_MAX_VOCAB)
+        return fail("sample_noalloc: n_vocab %d outside [1, %d] (the size of the static scratch)", (int)n_vocab,
+                    QMH_SAMPLE_NOALLOC_MAX_VOCAB);
+    /* parameter normalisation of qm_sampler_init (src/sampler.c:8-12) */
+    qmh_sampler s;
+    memset(&s, 0, sizeof s);
+    s.n_vocab = n_vocab;
+    s.temperature = temperature < 0 ? 0 : temperature;
+    s.top_k = top_k < 0 ? 0 : top_k;
+    s.top_p = (top_p <= 0 || top_p > 1) ? 1.0f : top_p;
+    if (sampler_greedy(&s)) {
+        LCHK(qmh_launch_argmax(logits, n_vocab, out, NULL, NULL, 0, S(stream)));
+        return 0;
+    }
+    void *base = NULL;
+    LCHK(qmh_sample_scratch(&base));
+    qmh_sample_args a = sample_args(&s, logits);
+    a.rng = rng;
+    a.out = out;
+    a.diag = NULL;
+    LCHK(qmh_launch_sample_scratch(&a, base, S(stream)));
     return 0;
 }
 
