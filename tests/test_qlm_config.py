@@ -5,66 +5,10 @@ takes the configuration from it (src/model.c:8-21,35-53): a duplicated key's lat
 ignored, a first entry of the wrong type makes a required key "missing/invalid" and an optional
 one take its default. The files are generated models whose metadata table is rewritten here;
 the tensor table and data are kept byte for byte."""
-import struct
-
 import numpy as np
 import pytest
 
-U32, F32, STR, ARR = 0, 1, 2, 3
-
-
-def read_qlm(path):
-    """(kv entries [(key, type, raw value bytes)], tensor table bytes, data bytes) of a .qlm."""
-    b = open(path, "rb").read()
-    assert b[:4] == b"QLMF"
-    ver, n_kv, n_t, data_off = struct.unpack_from("<IIIQ", b, 4)
-    off = 24
-    kv = []
-    for _ in range(n_kv):
-        (kl,) = struct.unpack_from("<I", b, off)
-        key = b[off + 4:off + 4 + kl].decode()
-        off += 4 + kl
-        (ty,) = struct.unpack_from("<I", b, off)
-        off += 4
-        if ty in (U32, F32):
-            val = b[off:off + 4]
-            off += 4
-        elif ty == STR:
-            (n,) = struct.unpack_from("<I", b, off)
-            val = b[off:off + 4 + n]
-            off += 4 + n
-        else:
-            (n,) = struct.unpack_from("<I", b, off)
-            val = b[off:off + 4 + 4 * n]
-            off += 4 + 4 * n
-        kv.append((key, ty, val))
-    t0 = off
-    for _ in range(n_t):
-        (nl,) = struct.unpack_from("<I", b, off)
-        off += 4 + nl
-        _, nd = struct.unpack_from("<II", b, off)
-        off += 8 + 8 * nd + 8
-    return ver, kv, n_t, b[t0:off], b[data_off:]
-
-
-def write_qlm(path, ver, kv, n_t, table, data):
-    head = bytearray(b"QLMF" + struct.pack("<IIIQ", ver, len(kv), n_t, 0))
-    for key, ty, val in kv:
-        kb = key.encode()
-        head += struct.pack("<I", len(kb)) + kb + struct.pack("<I", ty) + val
-    head += table
-    data_off = (len(head) + 63) // 64 * 64
-    struct.pack_into("<Q", head, 16, data_off)
-    with open(path, "wb") as f:
-        f.write(bytes(head) + bytes(data_off - len(head)) + data)
-
-
-def u32(v):
-    return struct.pack("<I", v)
-
-
-def f32(v):
-    return struct.pack("<f", v)
+from _qlm import ARR, F32, STR, U32, f32, read_qlm, u32, write_qlm  # noqa: F401
 
 
 @pytest.fixture(scope="module")
