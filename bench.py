@@ -7,17 +7,20 @@ a 512-token random-id prompt, then greedy decode. One "step" is one decode token
 forward + argmax, replayed as one hipGraph, inputs resident in HBM); W untimed warmup steps,
 then exactly K timed steps at positions P..P+K-1.
 
-Prints one JSON line: decode tok/s (value), prefill tok/s, fraction of the HBM roofline,
-`roofline` for the dominant kernel (the fused RMSNorm + W1|W3 Q4_0 matvec + SwiGLU), and
-`cpu_baseline` = the compiled reference (best CPU ISA, all host cores) on a bounded sample.
+Prints one JSON line: decode tok/s (value), prefill tok/s (every position's logits computed, as the
+reference's prompt loop does; also with the last position's only), the fraction of the HBM roofline,
+`roofline` for the dominant kernel (the fused RMSNorm + W1|W3 Q4_0 matvec + SwiGLU), the prefill
+against the int8- and FP32-MFMA peaks, the reference bench's forward loop (logits copied to the host),
+the other BASELINE configs (c1-c4, c5b) as extra keys, and `cpu_baseline` = the compiled reference
+(best CPU ISA) on a bounded sample of the same workload.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5a] [--no-cpu]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5a] [--no-cpu] [--no-configs]
 """
 import argparse
 import json
 import os
 import shutil
-import subprocess
+import statistics
 import sys
 import tempfile
 import time
@@ -25,24 +28,48 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+HBM_PEAK_GBS = 8000.0      # MI355X published HBM3E bandwidth
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+FP32_MFMA_PEAK_TFS = 157.3  # MI355X dense fp32 MFMA
+VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9  # fp32 VALU lane operations per second (256 CUs x 4 SIMD x 16 lanes x 2.4 GHz)
+CPU_SHARE = 16  # host threads the GPU box allots one GPU's jobs
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def row_bytes(w, n):
+    bb = 18 if w.wtype == "q4_0" else 34 if w.wtype == "q8_0" else None
+    return (n + 31) // 32 * bb if bb else 4 * n
+
+
 def decode_bytes_per_token(w, positions):
     """Algorithmic HBM bytes of one decode token, averaged over `positions`: every weight
     stream + K and V reads up to pos + KV writes + norm gains + logits + one embedding row."""
     D, H, L, V, kvd = w.dim, w.hidden_dim, w.n_layers, w.vocab_size, w.kvd
-    bb = 18 if w.wtype == "q4_0" else 34 if w.wtype == "q8_0" else None
-    nb = lambda n: (n + 31) // 32
-    rb = (lambda n: nb(n) * bb) if bb else (lambda n: 4 * n)
+    rb = lambda n: row_bytes(w, n)
     weights = L * ((D + 2 * kvd) * rb(D) + D * rb(D) + 2 * H * rb(D) + D * rb(H)) + V * rb(D)
     kv_read = sum(2 * L * (p + 1) * kvd * 4 for p in positions) / len(positions)
     small = 2 * L * kvd * 4 + (2 * L + 1) * D * 4 + V * 4 + rb(D)
     return weights + kv_read + small, weights
+
+
+def prefill_flops(w, P, logits_rows):
+    """Prefill flops as the reference counts them: every matmul over P tokens, the output matmul over
+    logits_rows positions, attention 4*L*D per (query, key) pair of the causal prompt."""
+    D, H, L, V, kvd = w.dim, w.hidden_dim, w.n_layers, w.vocab_size, w.kvd
+    layer = 2 * D * D + 2 * kvd * D + 3 * H * D
+    return 2 * P * L * layer + 2 * logits_rows * V * D + 4 * L * D * P * (P + 1) // 2
+
+
+def prefill_valu_floor_s(w, P, logits_rows):
+    """The bitwise matmul epilogue's VALU floor: 4 operations (cvt, mul, mul, add) per (row, token,
+    block) in the reference's order, at the device's fp32 VALU rate."""
+    D, H, L, V, kvd = w.dim, w.hidden_dim, w.n_layers, w.vocab_size, w.kvd
+    nb = lambda n: (n + 31) // 32
+    rows_nb = L * ((2 * D + 2 * kvd) * nb(D) + 2 * H * nb(D) + D * nb(H))
+    return 4 * (P * rows_nb + logits_rows * V * nb(D)) / VALU_LANE_OPS
 
 
 def pmc_traffic(name):
@@ -57,8 +84,35 @@ def pmc_traffic(name):
     return None
 
 
-def cpu_baseline(path, w, threads, n_prompt, n_gen, q):
-    """The compiled reference (oracle/_ref/ref_driver) on a bounded sample of the workload."""
+def host_cpus():
+    """The host's CPU topology (from /proc/cpuinfo) and the cores this process may run on."""
+    logical, cores, model = 0, set(), "?"
+    phys = core = None
+    for line in open("/proc/cpuinfo"):
+        k, _, v = line.partition(":")
+        k, v = k.strip(), v.strip()
+        if k == "processor":
+            logical += 1
+        elif k == "physical id":
+            phys = v
+        elif k == "core id":
+            core = v
+        elif k == "model name":
+            model = v
+        elif not k and phys is not None and core is not None:
+            cores.add((phys, core))
+            phys = core = None
+    if phys is not None and core is not None:
+        cores.add((phys, core))
+    n_phys = len(cores) or logical
+    return {"model": model, "logical_cpus": logical, "physical_cores": n_phys,
+            "threads_per_core": round(logical / n_phys, 2) if n_phys else None,
+            "sockets": len({p for p, _ in cores}) or None, "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(path, w, q, P, G):
+    """The compiled reference (oracle/_ref/ref_driver) on a bounded sample of the workload: the median of
+    three runs on the box's CPU share of threads, and one single-thread run."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _bind import REF_DRIVER, ref_run
 
@@ -66,16 +120,129 @@ def cpu_baseline(path, w, threads, n_prompt, n_gen, q):
         return None
     flags = open("/proc/cpuinfo").read()
     isa = "avx512" if (" avx512f " in flags and " avx512bw " in flags and " avx512vl " in flags) else "avx2"
-    prompt = q.prompt_ids(n_prompt, w.vocab_size)
-    res, _ = ref_run(path, prompt, n_gen, isa=isa, threads=threads, max_seq=n_prompt + n_gen, logits=False,
-                     warm=True, timeout=600)
+    host = host_cpus()
+    threads = min(host["affinity"], CPU_SHARE)
+    Ps, Gs = min(P, 64), min(G, 32)
+    prompt = q.prompt_ids(Ps, w.vocab_size)
+    runs = []
+    for r in range(3):
+        res, _ = ref_run(path, prompt, Gs, isa=isa, threads=threads, max_seq=Ps + Gs, logits=False, warm=r == 0,
+                         timeout=900)
+        runs.append(res)
+        log(f"[bench] cpu baseline run {r}: decode {res['decode_tok_s']:.2f} prefill {res['prompt_tok_s']:.2f} tok/s")
+    P1, G1 = min(P, 8), min(G, 8)
+    one, _ = ref_run(path, prompt[:P1], G1, isa=isa, threads=1, max_seq=P1 + G1, logits=False, timeout=900)
+    log(f"[bench] cpu baseline 1 thread: decode {one['decode_tok_s']:.2f} prefill {one['prompt_tok_s']:.2f} tok/s")
+    dec = [r["decode_tok_s"] for r in runs]
+    pre = [r["prompt_tok_s"] for r in runs]
     return {
-        "value": round(res["decode_tok_s"], 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-        "isa": res["isa"], "prefill_tok_s": round(res["prompt_tok_s"], 3),
-        "sample": f"same {w.name} .qlm file; {n_prompt} prompt tokens (sequential qm_model_forward) + {n_gen} "
-                  f"greedy decode steps, max_seq {n_prompt + n_gen}, QUILLM isa {res['isa']}, {threads} threads",
-        "tokens": res["tokens"],
+        "value": round(statistics.median(dec), 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+        "isa": runs[0]["isa"], "prefill_tok_s": round(statistics.median(pre), 3),
+        "runs_decode_tok_s": [round(x, 3) for x in dec], "runs_prefill_tok_s": [round(x, 3) for x in pre],
+        "one_thread": {"decode_tok_s": round(one["decode_tok_s"], 3), "prefill_tok_s": round(one["prompt_tok_s"], 3),
+                       "sample": f"{P1} prompt + {G1} decode tokens"},
+        "host": host,
+        "sample": f"same {w.name} .qlm file; {Ps} prompt tokens (sequential qm_model_forward, logits at every "
+                  f"position) + {Gs} greedy decode steps, max_seq {Ps + Gs}, QUILLM isa {runs[0]['isa']}, {threads} "
+                  f"threads (the box's CPU share for one GPU), median of 3 runs after one untimed warm pass",
     }
+
+
+def model_path(w, tag):
+    need = 8.5e9 if w.wtype == "q8_0" and w.dim >= 4096 else 4.5e9
+    d = "/dev/shm" if shutil.disk_usage("/dev/shm").free > 2 * need else tempfile.gettempdir()
+    return os.path.join(d, f"qmh_bench_{tag}_{w.name}_{os.getpid()}.qlm")
+
+
+def measure(q, w, P, K, W, detail=False):
+    """Prefill, decode and the forward loop of one config; with detail, the c5a extras too."""
+    import numpy as np
+
+    path = model_path(w, "m")
+    threads = min(len(os.sched_getaffinity(0)), CPU_SHARE)
+    t0 = time.time()
+    q.gen_model(path, w.config(), w.wtype, seed=w.seed, threads=threads)
+    gen_s = time.time() - t0
+    max_seq = min(P + max(K, W), w.max_seq)
+    K = min(K, max_seq - P)
+    out = {"workload": w.name, "prompt": P, "decode_steps": K, "max_seq": max_seq}
+    try:
+        t0 = time.time()
+        m = q.Model.load(path, max_seq=max_seq)
+        load_s = time.time() - t0
+        prompt = q.prompt_ids(P, w.vocab_size)
+        m.time_prefill(prompt[:4], 0, "last")  # warm the launch paths
+        pf_all = statistics.median(m.time_prefill(prompt, 0, "all") for _ in range(3))
+        pf_last = statistics.median(m.time_prefill(prompt, 0, "last") for _ in range(3))
+        fwd = m.forward(int(prompt[-1]), P - 1)  # logits of the last prompt position
+        tok0 = int(np.argmax(fwd))
+        if W > 0:
+            m.greedy(tok0, P, min(W, K))
+        ids, dev_ms = m.time_greedy(tok0, P, K)
+        value = K / (dev_ms / 1e3)
+        fids, fwd_ms = m.time_forward(tok0, P, K)
+        assert list(fids) == list(ids), "forward loop and device greedy loop disagree"
+        bpt, wbytes = decode_bytes_per_token(w, list(range(P, P + K)))
+        out.update({
+            "decode_tok_s": round(value, 2), "ms_per_step": round(dev_ms / K, 4),
+            "decode_bytes_per_token": int(bpt), "decode_hbm_frac": round(value * bpt / (HBM_PEAK_GBS * 1e9), 4),
+            "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
+            "forward_tok_s": round(K / (fwd_ms / 1e3), 2),
+            "prefill_tok_s": round(P / (pf_all / 1e3), 2), "prefill_ms": round(pf_all, 3),
+            "prefill_last_logits_tok_s": round(P / (pf_last / 1e3), 2),
+            "greedy_ids_head": [int(x) for x in ids[:8]],
+        })
+        log(f"[bench] {w.name}: prefill {P} in {pf_all:.2f} ms (all logits) / {pf_last:.2f} ms (last), decode "
+            f"{value:.1f} tok/s ({out['decode_hbm_frac']:.3f} of HBM), forward loop {out['forward_tok_s']:.1f} tok/s")
+        if detail:
+            flops = prefill_flops(w, P, P)
+            ach = flops / (pf_all * 1e-3)
+            out["prefill_roofline"] = {
+                "bound": "mfma", "unit": "TOP/s", "achieved": round(ach / 1e12, 2), "peak": INT8_PEAK_TOPS,
+                "frac": round(ach / 1e12 / INT8_PEAK_TOPS, 4), "flops": int(flops),
+                "frac_of_fp32_mfma": round(ach / 1e12 / FP32_MFMA_PEAK_TFS, 4),
+                "valu_floor_ms": round(prefill_valu_floor_s(w, P, P) * 1e3, 3),
+                "note": "int8 MFMA block dots (exact) + the bitwise f32 epilogue on the VALU (4 ops per row, token, "
+                        "block); flops counted as the reference's P forwards, every position's logits included",
+            }
+            # the same steps sampled on the device with the reference CLI's default sampler
+            # (src/main.c:70-72: temperature 0.8, top-k 0, top-p 0.95, seed 42); wall clock, synchronous
+            with q.Sampler(w.vocab_size, 0.8, 0, 0.95, 42) as smp:
+                m.sample(smp, tok0, P, min(W, 8))
+                t0 = time.perf_counter()
+                m.sample(smp, tok0, P, K)
+                out["sampled_decode_tok_s"] = round(K / (time.perf_counter() - t0), 2)
+            # batched decode of 4 and 16 independent sequences (qmh_batch_greedy): informational
+            batched = []
+            for BB in (4, 16):
+                with q.Batch(m, BB) as bt:
+                    bt.greedy([tok0] * BB, [P] * BB, 2)
+                    _, b_ms = bt.greedy([tok0] * BB, [P] * BB, K)
+                batched.append({"sequences": BB, "tok_s_aggregate": round(BB * K / (b_ms / 1e3), 1),
+                                "ms_per_step": round(b_ms / K, 3)})
+            out["batched_decode"] = batched
+            stages = {}
+            for st in ("qkv", "wo", "w13", "w2", "output", "attn_scores", "attn_pv"):
+                ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=P + K - 1)
+                stages[st] = {"us_per_launch": round(ms * 1e3, 3),
+                              "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1) if nbytes else None,
+                              "weight_MB": round(nbytes / 1e6, 3)}
+            out["stages"] = stages
+            ms_w13, bytes_w13 = m.time_stage("w13", 3 * w.n_layers, pos=P + K - 1)
+            achieved = bytes_w13 / (ms_w13 * 1e-3) / 1e9
+            out["roofline"] = {
+                "kernel": "k_matvec<Q4_0> W1|W3 launch (64-row tiles: RMSNorm + W1|W3 + SwiGLU + W2's quantized input)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": pmc_traffic(f"k_matvec_w13_{w.wtype}_{w.name}_pmc.txt"),
+                "bytes_per_launch": int(bytes_w13), "us_per_launch": round(ms_w13 * 1e3, 3)}
+            out["setup_s"] = {"generate": round(gen_s, 1), "load": round(load_s, 1)}
+        m.close()
+    except BaseException:
+        if os.path.exists(path):
+            os.remove(path)
+        raise
+    return out, path
 
 
 def main():
@@ -86,9 +253,7 @@ def main():
     ap.add_argument("--workload", default="c5a")
     ap.add_argument("--prefill", type=int, default=None, help="prompt length (default: the config's 512)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-prompt", type=int, default=None, help="CPU sample prompt (default: the same P)")
-    ap.add_argument("--cpu-gen", type=int, default=None, help="CPU sample decode steps (default: the same K)")
-    ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--probe-copy", action="store_true",
                     help="first run a known-size streaming kernel (fp16->fp32 of 64 Mi halves: 128 MiB read, "
                          "256 MiB written) whose FETCH_SIZE/WRITE_SIZE readings calibrate the counters")
@@ -97,8 +262,6 @@ def main():
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported by this build "
               "(the token loop runs on one MI355X; multi-GPU sharding is a design note, not a run)", file=sys.stderr)
         sys.exit(2)
-
-    import numpy as np
 
     import quillm_amd as q
 
@@ -119,93 +282,15 @@ def main():
         del src, dst
         log(f"[bench] probe copy: 3 x k_h2f over {n} halves")
 
-    # synthetic model file (generated on this host: it does not travel)
-    need = 8.5e9 if w.wtype == "q8_0" else 4.5e9
-    d = args.model_dir
-    if d is None:
-        d = "/dev/shm" if shutil.disk_usage("/dev/shm").free > 2 * need else tempfile.gettempdir()
-    path = os.path.join(d, f"qmh_bench_{w.name}_{os.getpid()}.qlm")
-    threads = min(os.cpu_count() or 1, 16)
-    t0 = time.time()
-    q.gen_model(path, w.config(), w.wtype, seed=w.seed, threads=threads)
-    gen_s = time.time() - t0
-    log(f"[bench] generated {w.name} ({os.path.getsize(path) / 1e9:.2f} GB) in {gen_s:.1f}s")
-    try:
-        max_seq = P + max(K, W)
-        t0 = time.time()
-        m = q.Model.load(path, max_seq=max_seq)
-        load_s = time.time() - t0
-        log(f"[bench] loaded to device in {load_s:.1f}s (max_seq {max_seq})")
-        prompt = q.prompt_ids(P, w.vocab_size)
-
-        # prefill: P tokens at positions 0..P-1 (warm the graph first)
-        m.prefill(prompt[:4], 0)
-        q.sync()
-        t0 = time.perf_counter()
-        last = m.prefill(prompt, 0, want_logits=False)
-        q.sync()
-        prefill_s = time.perf_counter() - t0
-        fwd = m.forward(int(prompt[-1]), P - 1)  # logits of the last prompt position
-        tok0 = int(np.argmax(fwd))
-        del last
-        log(f"[bench] prefill {P} tok in {prefill_s * 1e3:.1f} ms")
-
-        # decode: W warmup steps, then K timed steps from the same start (positions P..P+K-1)
-        if W > 0:
-            m.greedy(tok0, P, W)
-        q.sync()
-        t0 = time.perf_counter()
-        ids, dev_ms = m.time_greedy(tok0, P, K)
-        q.sync()
-        wall_s = time.perf_counter() - t0
-        ms_per_step = dev_ms / K
-        value = K / (dev_ms / 1e3)
-        log(f"[bench] decode {K} steps: {dev_ms:.2f} ms device ({wall_s * 1e3:.2f} ms wall), {value:.1f} tok/s")
-
-        # the same steps sampled on the device with the reference CLI's default sampler
-        # (src/main.c:70-72: temperature 0.8, top-k 0, top-p 0.95, seed 42); wall clock, synchronous
-        with q.Sampler(w.vocab_size, 0.8, 0, 0.95, 42) as smp:
-            m.sample(smp, tok0, P, min(W, 8))
-            t0 = time.perf_counter()
-            m.sample(smp, tok0, P, K)
-            sampled_s = time.perf_counter() - t0
-        log(f"[bench] sampled decode {K} steps: {sampled_s * 1e3:.2f} ms wall, {K / sampled_s:.1f} tok/s")
-
-        # batched decode of 4 and 16 independent sequences (qmh_batch_greedy) over the same positions:
-        # informational, the metric stays batch 1
-        batched = []
-        for BB in (4, 16):
-            with q.Batch(m, BB) as bt:
-                bt.greedy([tok0] * BB, [P] * BB, 2)
-                _, b_ms = bt.greedy([tok0] * BB, [P] * BB, K)
-            batched.append({"sequences": BB, "tok_s_aggregate": round(BB * K / (b_ms / 1e3), 1),
-                            "ms_per_step": round(b_ms / K, 3)})
-            log(f"[bench] batched decode B={BB}: {b_ms / K:.3f} ms per step, "
-                f"{BB * K / (b_ms / 1e3):.1f} tok/s aggregate")
-
-        # dominant kernel: fused RMSNorm + W1|W3 matvec + SwiGLU, cycling the layers
-        stages = {}
-        for st in ("qkv", "wo", "w13", "w2", "output", "attn_scores", "attn_pv"):
-            ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=P + K - 1)
-            stages[st] = {"us_per_launch": round(ms * 1e3, 3),
-                          "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1) if nbytes else None,
-                          "weight_MB": round(nbytes / 1e6, 3)}
-        ms_w13, bytes_w13 = m.time_stage("w13", 3 * w.n_layers, pos=P + K - 1)
-        achieved = bytes_w13 / (ms_w13 * 1e-3) / 1e9
-        m.close()
-    finally:
-        pass
-
-    positions = list(range(P, P + K))
-    bpt, wbytes = decode_bytes_per_token(w, positions)
+    head, path = measure(q, w, P, K, W, detail=True)
     out = {
         "metric": "decode tok/s + % HBM roofline, 7B-shape Q4_0 bs=1; prefill tok/s @512",
-        "value": round(value, 2),
+        "value": head["decode_tok_s"],
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": K,
+        "steps": head["decode_steps"],
         "warmup": W,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -213,36 +298,36 @@ def main():
         "data": "synthetic: random-init N(0,0.02) weights (seed 1), random prompt ids (seed 1234)",
         "config": {"workload": f"{w.name}: 7B-shape Llama {w.wtype} dim {w.dim} hidden {w.hidden_dim} "
                                f"{w.n_layers} layers {w.n_heads}/{w.n_kv_heads} heads vocab {w.vocab_size}, "
-                               f"batch 1, prompt {P}, decode {K} greedy",
-                   "prompt": P, "decode_steps": K, "max_seq": P + max(K, W)},
-        "prefill_tok_s": round(P / prefill_s, 2),
-        "sampled_decode_tok_s": round(K / sampled_s, 2),
-        "batched_decode": batched,
-        "decode_bytes_per_token": int(bpt),
-        "decode_hbm_frac": round(value * bpt / (HBM_PEAK_GBS * 1e9), 4),
-        "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
-        "roofline": {"kernel": "k_matvec<Q4_0> W1|W3 launch (64-row tiles: RMSNorm + W1|W3 + SwiGLU + W2's quantized input)",
-                     "bound": "hbm",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": pmc_traffic(f"k_matvec_w13_{w.wtype}_{w.name}_pmc.txt") if w.name in ("c5a", "c5b") else None,
-                     "bytes_per_launch": int(bytes_w13), "us_per_launch": round(ms_w13 * 1e3, 3)},
-        "stages": stages,
-        "greedy_ids_head": [int(x) for x in ids[:8]],
-        "setup_s": {"generate": round(gen_s, 1), "load": round(load_s, 1)},
+                               f"batch 1, prompt {P}, decode {head['decode_steps']} greedy",
+                   "prompt": P, "decode_steps": head["decode_steps"], "max_seq": head["max_seq"]},
     }
-    if not args.no_cpu:
-        cpu_threads = min(os.cpu_count() or 1, 16)
-        cp = P if args.cpu_prompt is None else args.cpu_prompt
-        cg = K if args.cpu_gen is None else args.cpu_gen
-        log(f"[bench] cpu baseline: reference, {cpu_threads} threads, {cp}+{cg} tokens")
-        cb = cpu_baseline(path, w, cpu_threads, cp, cg, q)
-        if cb is not None:
-            out["cpu_baseline"] = {k: v for k, v in cb.items() if k != "tokens"}
+    for k in ("prefill_tok_s", "prefill_last_logits_tok_s", "prefill_ms", "prefill_roofline", "forward_tok_s",
+              "sampled_decode_tok_s", "batched_decode", "decode_bytes_per_token", "decode_hbm_frac",
+              "decode_roofline_tok_s", "roofline", "stages", "greedy_ids_head", "setup_s"):
+        out[k] = head[k]
+    out["timing"] = ("decode: HIP events around K graph replays (device argmax, no host round trip); forward_tok_s: "
+                     "host clock around K qmh_model_forward calls with the logits copied to the host and a host "
+                     "argmax (the reference bench's loop, bench/bench.c:143-149); prefill: HIP events around the "
+                     "batched prefill, median of 3, every position's logits computed on the device (the work of the "
+                     "reference's prompt loop) or only the last one's")
     try:
+        if not args.no_cpu:
+            log(f"[bench] cpu baseline: reference on a sample of {w.name}")
+            cb = cpu_baseline(path, w, q, P, head["decode_steps"])
+            if cb is not None:
+                out["cpu_baseline"] = cb
+    finally:
         os.remove(path)
-    except OSError:
-        pass
+    if not args.no_configs:
+        others = {}
+        for name in ("c1", "c2", "c3", "c4", "c5a", "c5b"):
+            if name == w.name:
+                continue
+            wc = q.WORKLOADS[name]
+            r, p = measure(q, wc, wc.n_prompt, wc.n_gen, W)
+            os.remove(p)
+            others[name] = {k: v for k, v in r.items() if k != "workload"}
+        out["configs"] = others
     print(json.dumps(out), flush=True)
 
 

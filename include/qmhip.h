@@ -220,6 +220,14 @@ int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double
                          double *bytes_per_launch);
 /* qmh_model_greedy, with HIP events around the n_steps graph replays (*ms = their total). */
 int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms);
+/* qmh_model_prefill of n tokens at pos0, with HIP events around it (*ms). logits: 0 none, 1 the last
+ * position's, 2 every position's (the reference's prompt loop computes them all: src/main.c:127-130);
+ * they stay in device memory. */
+int qmh_model_time_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, int logits, double *ms);
+/* The reference bench's decode loop (bench/bench.c:143-149) on this model: n_steps of
+ * token = argmax(qmh_model_forward(token, pos + k)), the argmax on the host over the returned (copied)
+ * logits; *ms from a host clock; out (optional) receives the tokens. */
+int qmh_model_time_forward(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms);
 
 /* ------------------------------------------------------------------ synthetic models */
 

@@ -109,6 +109,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_model_time_stage": (ctypes.c_int, [vp, ctypes.c_int, i32, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                                 ctypes.POINTER(ctypes.c_double)]),
         "qmh_model_time_greedy": (ctypes.c_int, [vp, i32, i32, i32, vp, ctypes.POINTER(ctypes.c_double)]),
+        "qmh_model_time_prefill": (ctypes.c_int, [vp, vp, i32, i32, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+        "qmh_model_time_forward": (ctypes.c_int, [vp, i32, i32, i32, vp, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -251,6 +253,24 @@ class Model:
         ms = ctypes.c_double()
         _check(load_library().qmh_model_time_greedy(self._h, int(token), int(pos), int(n_steps), out.ctypes.data,
                                                      ctypes.byref(ms)), "time_greedy")
+        return out[:n_steps], ms.value
+
+    PREFILL_LOGITS = {"none": 0, "last": 1, "all": 2}
+
+    def time_prefill(self, tokens, pos0: int = 0, logits: str = "all") -> float:
+        """Device ms of a prefill of tokens at pos0 (logits computed on the device: none, last, all)."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        ms = ctypes.c_double()
+        _check(load_library().qmh_model_time_prefill(self._h, toks.ctypes.data, len(toks), int(pos0),
+                                                      self.PREFILL_LOGITS[logits], ctypes.byref(ms)), "time_prefill")
+        return ms.value
+
+    def time_forward(self, token: int, pos: int, n_steps: int):
+        """(ids, host ms) of the reference bench's loop: token = argmax(forward(token, pos+k)) on the host."""
+        out = np.zeros(max(n_steps, 1), np.int32)
+        ms = ctypes.c_double()
+        _check(load_library().qmh_model_time_forward(self._h, int(token), int(pos), int(n_steps), out.ctypes.data,
+                                                      ctypes.byref(ms)), "time_forward")
         return out[:n_steps], ms.value
 
     def close(self):

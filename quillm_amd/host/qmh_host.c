@@ -14,6 +14,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "../../include/qmhip.h"
 #include "../csrc/qmh_launch.h"
@@ -962,8 +963,11 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     return 0;
 }
 
-/* the prompt in passes of up to pf_cap tokens; logits (P x vocab) only when asked for */
-static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, float *logits) {
+/* the prompt in passes of up to pf_cap tokens. Logits (mode): none; the last position's; or every
+ * position's (the reference's prompt loop computes them all), into d_pf_logits and, when host is given,
+ * copied there (host[V] for the last, host[n*V] for all) */
+enum { PF_LOGITS_NONE = 0, PF_LOGITS_LAST = 1, PF_LOGITS_ALL = 2 };
+static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, int mode, float *host) {
     const qmh_config *c = &m->cfg;
     const int D = c->dim, V = c->vocab_size;
     for (int32_t c0 = 0; c0 < n; c0 += m->pf_cap) {
@@ -973,10 +977,13 @@ static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
         LCHK(qmh_launch_pf_embed(m->d_embd, m->emb_dtype, D, V, m->d_pf_tok, P, m->d_pf_x, g_stream));
         for (int l = 0; l < c->n_layers; l++)
             if (pf_layer(m, l, P, pos, NULL, g_stream)) return -1;
-        if (logits) { /* logits = Woutput rmsnorm(x) for every position (src/model.c:188-189) */
+        const int last = c0 + P == n;
+        if (mode == PF_LOGITS_ALL || (mode == PF_LOGITS_LAST && last)) {
+            /* logits = Woutput rmsnorm(x) (src/model.c:188-189): every position, or the last one */
+            const int rows = mode == PF_LOGITS_ALL ? P : 1;
             qmh_pf_args a;
-            pf_args_for(m, &m->output, P, &a);
-            a.xf = m->d_pf_x;
+            pf_args_for(m, &m->output, rows, &a);
+            a.xf = m->d_pf_x + (size_t)(P - rows) * D;
             a.ldxf = D;
             a.nxf = D;
             a.norm_w = m->d_norms + (size_t)(2 * c->n_layers) * D;
@@ -986,8 +993,9 @@ static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
             a.out0 = m->d_pf_logits;
             a.ld0 = V;
             LCHK(qmh_launch_pf_gemm(&a, g_stream));
-            HIPCHK(hipMemcpyAsync(logits + (size_t)c0 * V, m->d_pf_logits, sizeof(float) * (size_t)P * V,
-                                  hipMemcpyDeviceToHost, g_stream));
+            if (host)
+                HIPCHK(hipMemcpyAsync(host + (mode == PF_LOGITS_ALL ? (size_t)c0 * V : 0), m->d_pf_logits,
+                                      sizeof(float) * (size_t)rows * V, hipMemcpyDeviceToHost, g_stream));
         }
         HIPCHK(hipStreamSynchronize(g_stream)); /* h_pf_tok is reused by the next pass */
     }
@@ -998,7 +1006,8 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
     if (!m || !tokens || n < 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.max_seq) return fail("prefill: bad range");
     for (int32_t i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) return fail("prefill: token %d out of range", tokens[i]);
-    if (m->pf_ok && getenv("QMH_PREFILL_SEQ") == NULL) return pf_batched(m, tokens, n, pos0, logits);
+    if (m->pf_ok && getenv("QMH_PREFILL_SEQ") == NULL)
+        return pf_batched(m, tokens, n, pos0, logits ? PF_LOGITS_ALL : PF_LOGITS_NONE, logits);
     const size_t V = (size_t)m->cfg.vocab_size;
     for (int32_t i = 0; i < n; i++) {
         int32_t *slot = m->h_tokpos + 4 * (size_t)i;
@@ -1023,6 +1032,63 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
     if (n_steps > 0 && out)
         HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
     HIPCHK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int qmh_model_time_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, int logits, double *ms) {
+    if (!m || !tokens || n < 1 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.max_seq || logits < 0 || logits > 2)
+        return fail("time_prefill: bad arguments");
+    for (int32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) return fail("time_prefill: token %d out of range", tokens[i]);
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    hipError_t e = hipEventRecord(e0, g_stream);
+    int rc = 0;
+    if (e == hipSuccess) {
+        if (m->pf_ok) {
+            rc = pf_batched(m, tokens, n, pos0, logits, NULL);
+        } else { /* the sequential path computes every position's logits anyway */
+            for (int32_t i = 0; i < n && e == hipSuccess; i++) {
+                int32_t *slot = m->h_tokpos + 4 * (size_t)i;
+                slot[0] = tokens[i];
+                slot[1] = pos0 + i;
+                e = hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream);
+                if (e == hipSuccess) e = run_step(m, 0);
+            }
+        }
+    }
+    if (e == hipSuccess && rc == 0) e = hipEventRecord(e1, g_stream);
+    if (e == hipSuccess && rc == 0) e = hipEventSynchronize(e1);
+    float t = 0.0f;
+    if (e == hipSuccess && rc == 0) e = hipEventElapsedTime(&t, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc) return -1;
+    if (e != hipSuccess) return fail("time_prefill: %s", hipGetErrorString(e));
+    if (ms) *ms = (double)t;
+    return 0;
+}
+
+int qmh_model_time_forward(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms) {
+    if (!m || n_steps < 1 || token < 0 || token >= m->cfg.vocab_size || pos < 0 ||
+        (int64_t)pos + n_steps > m->cfg.max_seq)
+        return fail("time_forward: bad token/range");
+    const int V = m->cfg.vocab_size;
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    int32_t tok = token;
+    for (int32_t k = 0; k < n_steps; k++) {
+        const float *lg = qmh_model_forward(m, tok, pos + k);
+        if (!lg) return -1;
+        int best = 0; /* qm_argmax (src/sampler.c:27-32) on the host, as bench/bench.c:147 does */
+        for (int i = 1; i < V; i++)
+            if (lg[i] > lg[best]) best = i;
+        tok = best;
+        if (out) out[k] = tok;
+    }
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    if (ms) *ms = (double)(t1.tv_sec - t0.tv_sec) * 1e3 + (double)(t1.tv_nsec - t0.tv_nsec) * 1e-6;
     return 0;
 }
 
