@@ -1,0 +1,197 @@
+"""Index bounds of the decode attention kernels, modelled on the CPU (no GPU).
+
+Every global and LDS index the kernels below compute is enumerated over the whole grid, every
+thread and every unrolled load, for each model shape the library runs (the BASELINE configs and
+the test models) and positions on both sides of each chunk boundary, and checked against the
+extent of its buffer: the per-layer caches K [kvd][max_seq] and V [max_seq][kvd], the scores
+att [n_heads][max_seq], q and out [n_heads*head_dim], and the dynamic LDS bytes the launcher
+passes. The formulas restate the kernels' own index arithmetic, line by line:
+  * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:24-61 (launcher :63-89)
+  * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:368-396 (launcher :399-415): clamped float4 K
+                          loads past the last position (t <= max_seq-4)
+  * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:92-246 (k_attn_pv :249-256): unconditional V
+                          and score loads clamped to position n-1 / score 0, columns to head_dim-1
+  * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:267-397: float4 V loads clamped to position
+                          n-1 and column head_dim-4, pieces of 128 staged products
+  * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:399-417: kernel choice and dynamic LDS
+This is a model: a kernel edit that changes an index must change it here too.
+"""
+import numpy as np
+import pytest
+
+WG, SC_T, CW = 256, 64, 16
+
+# (n_heads, n_kv_heads, head_dim, max_seq): BASELINE configs c1-c5 and the test models
+SHAPES = [
+    (6, 6, 48, 256), (6, 2, 48, 256), (12, 12, 64, 1024), (32, 4, 64, 2048), (32, 32, 128, 4096),
+    (4, 2, 16, 64), (6, 3, 12, 64), (3, 3, 32, 48), (12, 1, 8, 300), (4, 2, 48, 136),
+    (2, 2, 128, 1300), (6, 6, 10, 700), (4, 2, 32, 700), (32, 32, 128, 640),
+]
+POSITIONS = [0, 1, 2, 3, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 575, 639, 640, 641, 700,
+             767, 768, 1023, 1024, 1279, 1280, 1281, 2047, 4095]
+
+
+def positions(S):
+    return sorted({p for p in POSITIONS if p < S} | {S - 2, S - 1} - {-1})
+
+
+class Extents:
+    def __init__(self, nh, nkv, hd, S):
+        self.K = nkv * hd * S
+        self.V = S * nkv * hd
+        self.att = nh * S
+        self.q = nh * hd
+        self.out = nh * hd
+
+
+def inb(what, idx, size):
+    idx = np.asarray(idx)
+    if idx.size == 0:
+        return
+    lo, hi = int(idx.min()), int(idx.max())
+    assert lo >= 0 and hi < size, f"{what}: index range [{lo}, {hi}] outside [0, {size})"
+
+
+def scores(nh, nkv, hd, S, pos, ext):
+    """qmh_launch_attn_scores: the K-tile kernel for grouped heads, else the one-wave kernel."""
+    group = nh // nkv
+    t0 = np.arange(0, S, SC_T)  # blockIdx.y * 64
+    t0 = t0[t0 <= pos]  # workgroups past pos return at once
+    kvh = np.arange(nkv)
+    if nh > nkv and S % 4 == 0 and S >= 4 and hd in (128, 64, 48):
+        L4 = hd * SC_T // 4 // WG
+        e = (np.arange(L4)[:, None] * WG + np.arange(WG)[None, :]).ravel()
+        i, p4 = e // (SC_T // 4), e % (SC_T // 4)
+        t = t0[:, None] + 4 * p4[None, :]
+        tc = np.minimum(t, S - 4)
+        for r in range(4):  # the float4's four floats
+            inb("scores_t K", kvh[:, None, None] * hd * S + i[None, None, :] * S + tc[None, :, :] + r, ext.K)
+        inb("scores_t LDS kt", i * SC_T + 4 * p4 + 3, hd * SC_T)
+        lane = np.arange(64)
+        inb("scores_t LDS read", (hd - 1) * SC_T + lane, hd * SC_T)
+    else:
+        lane = np.arange(SC_T)
+        t = t0[:, None] + lane[None, :]
+        tc = np.minimum(t, S - 1)
+        d = np.arange(hd)
+        inb("scores K", kvh[:, None, None] * hd * S + d[None, :, None] * S + tc.ravel()[None, None, :], ext.K)
+    hl = np.arange(group)
+    inb("scores q", (kvh[:, None] * group + hl[None, :]) * hd + hd - 1, ext.q)
+    tw = (t0[:, None] + np.arange(SC_T)[None, :]).ravel()
+    tw = tw[tw <= pos]
+    inb("scores att", (kvh[:, None, None] * group + hl[None, :, None]) * S + tw[None, None, :], ext.att)
+
+
+def pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats):
+    """attn_pv_chunks<TC, MHA> over grid (nkv, ceil(hd/16)) x 256 threads."""
+    group, kvd = nh // nkv, hd * nkv
+    tid = np.arange(WG)
+    kvh = np.arange(nkv)
+    i0 = np.arange(0, hd, CW)
+    # first head's scores, 4 per thread, clamped to 0
+    t = tid[None, :] + WG * np.arange(4)[:, None]
+    inb("pv sv", (kvh[:, None] * group) * S + np.where(t < n, t, 0).ravel()[None, :], ext.att)
+    LPT = TC * CW // WG
+    e = (np.arange(LPT)[:, None] * WG + tid[None, :]).ravel()
+    te, cce = e // CW, e % CW
+    colc_e = np.minimum(i0[:, None] + (e % CW)[None, :], hd - 1)  # e % 16 == threadIdx % 16
+    for T0 in range(0, n, TC):
+        tcl = np.minimum(T0 + te, n - 1)
+        inb("pv V", tcl[None, None, :] * kvd + kvh[:, None, None] * hd + colc_e[None, :, :], ext.V)
+        nt = min(TC, n - T0)
+        if not (MHA and T0 == 0):
+            hl, tt = e[e < group * TC] // TC, e[e < group * TC] % TC
+            inb("pv P", hl * TC + tt, group * TC)
+            tt_on = tt < nt
+            inb("pv att", (kvh[:, None] * group + hl[None, tt_on]) * S + T0 + tt[None, tt_on], ext.att)
+        else:
+            tp = tid[None, :] + WG * np.arange(4)[:, None]
+            inb("pv P first", tp[tp < TC], group * TC)
+        inb("pv Vs", group * TC + cce * (TC + 4) + te, lds_floats)
+        n32 = (nt + 31) >> 5
+        last = 4 * (8 * (n32 - 1) + 7) + 3
+        chain = tid[tid < group * CW]
+        inb("pv chain P", (chain // CW) * TC + last, group * TC)
+        inb("pv chain Vs", group * TC + (chain % CW) * (TC + 4) + last, lds_floats)
+    ch = tid[tid < group * CW]
+    col = ch % CW
+    ok = (i0[:, None] + col[None, :]) < hd
+    outi = (kvh[:, None, None] * group + (ch // CW)[None, None, :]) * hd + i0[None, :, None] + col[None, None, :]
+    inb("pv out", outi[np.broadcast_to(ok[None], outi.shape)], ext.out)
+
+
+def pv_mha(TC, nh, hd, S, n, ext, lds_floats):
+    """k_attn_pv_mha<TC> for n <= TC (longer contexts take attn_pv_chunks<TC, true>)."""
+    kvd = hd * nh
+    tid = np.arange(WG)
+    h = np.arange(nh)
+    i0 = np.arange(0, hd, CW)
+    SK = (TC + WG - 1) // WG
+    t = tid[None, :] + WG * np.arange(SK)[:, None]
+    inb("mha sv", h[:, None] * S + np.where(t < n, t, 0).ravel()[None, :], ext.att)
+    c = i0[:, None] + 4 * (tid & 3)[None, :]
+    cc = np.where(c <= hd - 4, c, hd - 4)
+    L4 = TC * CW // 4 // WG
+    tv = np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :]
+    tcl = np.minimum(tv, n - 1)
+    for r in range(4):  # the float4's four floats
+        inb("mha V", tcl[None, None, :, :] * kvd + h[:, None, None, None] * hd + cc[None, :, None, :] + r, ext.V)
+    inb("mha P", np.arange(n), TC)
+    PC = 128
+    npc = (n + PC - 1) // PC
+    for j in range(npc):
+        for u in range(2):
+            ts = (2 * j + u) * (WG // 4) + (tid >> 2)
+            assert ts.max() < TC
+            for r in range(4):
+                inb("mha Vs stage", TC + (4 * (tid & 3) + r) * (TC + 4) + ts, lds_floats)
+        q = np.arange(PC // 4)
+        inb("mha chain", TC + np.arange(CW)[:, None] * (TC + 4) + 4 * (j * (PC // 4) + q)[None, :] + 3, lds_floats)
+    # float4 staging rows and chain rows stay 16-byte aligned
+    assert (TC % 4, (TC + 4) % 4) == (0, 0)
+    ok = (i0[:, None] + np.arange(CW)[None, :]) < hd
+    outi = h[:, None, None] * hd + i0[None, :, None] + np.arange(CW)[None, None, :]
+    inb("mha out", outi[np.broadcast_to(ok[None], outi.shape)], ext.out)
+
+
+LDS_MAX = 160 * 1024 - 1024  # per workgroup on gfx950, less the kernels' static LDS
+
+
+def pv(nh, nkv, hd, S, pos, ext):
+    """qmh_launch_attn_pv's choice of kernel and dynamic LDS bytes."""
+    group = nh // nkv
+    assert group <= 16 and group * CW <= WG
+    n = pos + 1
+    if group == 1 and hd % 4 == 0:
+        lds_floats = 640 + CW * (640 + 4)
+        assert 4 * lds_floats <= LDS_MAX
+        if n <= 640:
+            pv_mha(640, nh, hd, S, n, ext, lds_floats)
+        else:
+            pv_chunks(640, True, nh, nh, hd, S, n, ext, lds_floats)
+        return
+    TC, MHA = (640, True) if group == 1 else (640, False) if group <= 8 else (256, False)
+    lds_floats = group * TC + CW * (TC + 4)
+    assert 4 * lds_floats <= LDS_MAX
+    pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_decode_attention_indices_in_bounds(shape):
+    nh, nkv, hd, S = shape
+    ext = Extents(nh, nkv, hd, S)
+    for pos in positions(S):
+        scores(nh, nkv, hd, S, pos, ext)
+        pv(nh, nkv, hd, S, pos, ext)
+
+
+def test_model_catches_an_out_of_range_clamp():
+    """The check is not vacuous: in the K-tile kernel with max_seq = 136, the last tile's float4s
+    start at positions 128 .. 188; clamped to max_seq-1 instead of max_seq-4 the last one reads
+    three floats past the cache."""
+    nh, nkv, hd, S = 4, 2, 48, 136
+    t = 128 + 4 * np.arange(16)
+    K = Extents(nh, nkv, hd, S).K
+    inb("kept clamp", (nkv - 1) * hd * S + (hd - 1) * S + np.minimum(t, S - 4) + 3, K)
+    with pytest.raises(AssertionError):
+        inb("planted clamp", (nkv - 1) * hd * S + (hd - 1) * S + np.minimum(t, S - 1) + 3, K)
