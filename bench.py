@@ -15,6 +15,8 @@ the other BASELINE configs (c1-c4, c5b) as extra keys, and `cpu_baseline` = the 
 (best CPU ISA) on a bounded sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5a] [--no-cpu] [--no-configs]
+  python bench.py --probe-stream        the read ceiling for the weight sizes (probe line, then exit)
+  python bench.py --probe-stages POS    the decode stages' times at position POS (probe line, then exit)
 """
 import argparse
 import json
@@ -245,6 +247,70 @@ def measure(q, w, P, K, W, detail=False):
     return out, path
 
 
+def probe_stream(q, w, grids=(256, 512, 1024), reps=20):
+    """The device's read ceiling for the sizes of the decode step's weight streams (the separate probe
+    library quillm_amd/libqmhprobe.so, so the token loop's code objects stay as timed): each size alone,
+    launches back to back, every launch reading a fresh stretch of a 2 GiB pool (HBM, not the 256 MB
+    Infinity Cache); and one layer's four matrices in order, 32 layers back to back."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "quillm_amd", "libqmhprobe.so"))
+    lib.qmh_probe_reads.restype = ctypes.c_int
+    lib.qmh_probe_reads.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    D, H, kvd = w.dim, w.hidden_dim, w.kvd
+    rb = lambda n: row_bytes(w, n)
+    mats = {"qkv": (D + 2 * kvd) * rb(D), "wo": D * rb(D), "w13": 2 * H * rb(D), "w2": D * rb(H),
+            "output": w.vocab_size * rb(D), "1GiB": 1 << 30}
+    pool_bytes = 2 << 30
+    pool = q.DeviceBuffer(pool_bytes)
+    q._check(q.load_library().qmh_memset(pool.ptr, 1, pool_bytes), "probe fill")
+    q.sync()
+    out = {"probe": "stream", "kernel": "k_read (16-byte loads, 4 in flight per lane, 256-thread workgroups)",
+           "pool_bytes": pool_bytes, "reps": reps, "single": {}}
+    for name, nbytes in mats.items():
+        n16 = (nbytes + 15) // 16 * 16
+        arr = (ctypes.c_uint64 * 1)(n16)
+        per = {}
+        for g in grids:
+            us = (ctypes.c_double * 1)()
+            rc = lib.qmh_probe_reads(ctypes.c_void_p(pool.ptr), pool_bytes, arr, 1, reps, g, 0, us)
+            if rc:
+                raise RuntimeError(f"qmh_probe_reads: {rc}")
+            per[str(g)] = round(us[0], 2)
+        best = min(per.values())
+        out["single"][name] = {"bytes": n16, "us_by_grid": per, "best_us": best,
+                               "best_GBps": round(n16 / (best * 1e-6) / 1e9, 1)}
+        log(f"[bench] probe stream {name}: {n16 / 1e6:.2f} MB, best {best:.2f} us ({out['single'][name]['best_GBps']} GB/s)")
+    seq = [mats[k] for k in ("qkv", "wo", "w13", "w2")]
+    arr = (ctypes.c_uint64 * 4)(*[(n + 15) // 16 * 16 for n in seq])
+    us = (ctypes.c_double * 1)()
+    rc = lib.qmh_probe_reads(ctypes.c_void_p(pool.ptr), pool_bytes, arr, 4, w.n_layers, 512, 1, us)
+    if rc:
+        raise RuntimeError(f"qmh_probe_reads: {rc}")
+    out["layer_sequence"] = {"matrices": ["qkv", "wo", "w13", "w2"], "grid": 512, "layers": w.n_layers,
+                             "bytes": int(sum(arr)), "us_per_layer": round(us[0], 2),
+                             "GBps": round(sum(arr) / (us[0] * 1e-6) / 1e9, 1)}
+    del pool
+    return out
+
+
+def probe_stages(q, w, pos):
+    """Stage times of the decode step at position pos (HIP events over 3 x n_layers launches cycling the
+    layers), for counter runs of single kernels at a chosen context length."""
+    path = model_path(w, "p")
+    try:
+        q.gen_model(path, w.config(), w.wtype, seed=w.seed, threads=min(len(os.sched_getaffinity(0)), CPU_SHARE))
+        out = {"probe": "stages", "workload": w.name, "pos": pos, "stages": {}}
+        with q.Model.load(path, max_seq=pos + 1) as m:
+            for st in ("qkv", "wo", "w13", "w2", "output", "attn_scores", "attn_pv"):
+                ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=pos)
+                out["stages"][st] = round(ms * 1e3, 3)
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +320,10 @@ def main():
     ap.add_argument("--prefill", type=int, default=None, help="prompt length (default: the config's 512)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--probe-stream", action="store_true",
+                    help="print the device's read ceiling for the decode step's weight sizes and exit")
+    ap.add_argument("--probe-stages", type=int, default=None, metavar="POS",
+                    help="print the decode stages' times at position POS and exit")
     ap.add_argument("--probe-copy", action="store_true",
                     help="first run a known-size streaming kernel (fp16->fp32 of 64 Mi halves: 128 MiB read, "
                          "256 MiB written) whose FETCH_SIZE/WRITE_SIZE readings calibrate the counters")
@@ -281,6 +351,12 @@ def main():
         q.sync()
         del src, dst
         log(f"[bench] probe copy: 3 x k_h2f over {n} halves")
+    if args.probe_stream:
+        print(json.dumps(probe_stream(q, w)), flush=True)
+        return
+    if args.probe_stages is not None:
+        print(json.dumps(probe_stages(q, w, args.probe_stages)), flush=True)
+        return
 
     head, path = measure(q, w, P, K, W, detail=True)
     out = {
