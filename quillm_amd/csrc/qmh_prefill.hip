@@ -247,24 +247,35 @@ __device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLan
     }
 }
 
-// one block into the chains: s = s + (float)acc * (dw * dx) per (row, token) pair
+// one block into the chains: s = s + (float)acc * (dw * dx) per (row, token) pair. The MFMAs of
+// row tile q+1 (each into its own registers) are issued before the epilogue of row tile q, so the
+// multiplies run under the float work instead of each waiting for the previous results to be
+// consumed. Every accumulator's chain stays in block order.
 template <int WT, int NM, int NR, int TW>
 __device__ __forceinline__ void pf_mul(const PfBlock<NM, NR, TW> &cur, float (&s)[NM][NR][TW][4]) {
+    constexpr int Q = NM * NR;  // row tiles (m, r) = (q / NR, q % NR)
+    pf_v4i acc[2][TW];
+    auto issue = [&](int q, pf_v4i(&d)[TW]) {
+        const long Am = WT == QMH_Q8 ? cur.A[q / NR][q % NR] : pf_q4_operand((uint32_t)cur.A[q / NR][q % NR]);
 #pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m][r].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].x >> 16)),
-                                 qmh_h2f((uint16_t)(cur.sc[m][r].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].y >> 16))};
-            const long Am = WT == QMH_Q8 ? cur.A[m][r] : pf_q4_operand((uint32_t)cur.A[m][r]);
-#pragma unroll
-            for (int tt = 0; tt < TW; tt++) {
-                const pf_v4i z = {0, 0, 0, 0};
-                const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, cur.B[tt], z, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; e++) s[m][r][tt][e] = s[m][r][tt][e] + (float)acc[e] * (dw[e] * cur.dx[tt]);
-            }
+        for (int tt = 0; tt < TW; tt++) {
+            const pf_v4i z = {0, 0, 0, 0};
+            d[tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, cur.B[tt], z, 0, 0, 0);
         }
+    };
+    issue(0, acc[0]);
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        if (q + 1 < Q) issue(q + 1, acc[(q + 1) & 1]);
+        const int m = q / NR, r = q % NR;
+        const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m][r].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].x >> 16)),
+                             qmh_h2f((uint16_t)(cur.sc[m][r].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].y >> 16))};
+#pragma unroll
+        for (int tt = 0; tt < TW; tt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                s[m][r][tt][e] = s[m][r][tt][e] + (float)acc[q & 1][tt][e] * (dw[e] * cur.dx[tt]);
+    }
 }
 
 // one output of the matmul: y = row's value for token p (up: the W3 value of the SwiGLU pair;
@@ -409,23 +420,33 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 #pragma unroll
             for (int j = 0; j < PD; j++) {
                 const int jb = 8 * (k0 + j) + wave;
-                if (jb < nr)  // uniform per wave
+                if (jb < nr) {  // uniform per wave
+                    // every MFMA of the block first, each into its own registers, then the terms:
+                    // the multiplies overlap instead of each waiting for the previous results
+                    pf_v4i acc[NM][TT];
 #pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    const uint2 sc = blk[j].sc[m][0];
-                    const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
-                                         qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
-                    const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
+                    for (int m = 0; m < NM; m++) {
+                        const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
 #pragma unroll
-                    for (int tt = 0; tt < TT; tt++) {
-                        const pf_v4i z = {0, 0, 0, 0};
-                        const pf_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[tt], z, 0, 0, 0);
-                        const int p = 16 * tt + tok;
-                        if (p < P)
+                        for (int tt = 0; tt < TT; tt++) {
+                            const pf_v4i z = {0, 0, 0, 0};
+                            acc[m][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[tt], z, 0, 0, 0);
+                        }
+                    }
 #pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                T[(((size_t)m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
-                                    (float)acc[e] * (dw[e] * blk[j].dx[tt]);
+                    for (int m = 0; m < NM; m++) {
+                        const uint2 sc = blk[j].sc[m][0];
+                        const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
+                                             qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
+#pragma unroll
+                        for (int tt = 0; tt < TT; tt++) {
+                            const int p = 16 * tt + tok;
+                            if (p < P)
+#pragma unroll
+                                for (int e = 0; e < 4; e++)
+                                    T[(((size_t)m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
+                                        (float)acc[m][tt][e] * (dw[e] * blk[j].dx[tt]);
+                        }
                     }
                 }
             }
