@@ -254,9 +254,136 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
     attn_pv_chunks<TC, MHA>(att, V, out, n, n_heads, n_kv, hd, max_seq);
 }
 
-// One query head per kv head, head_dim a multiple of 4, and (tested on the device) a context of
-// at most TC positions; longer contexts take attn_pv_chunks. Same sums in the same order, laid
-// out for a shorter critical path:
+// k_attn_pv_mha past TC positions, up to QMH_PV_LONG: the same sums in the same order, streamed.
+// The statistics pass keeps every exponential e_t in LDS (P, n floats). V arrives in pieces of 128
+// positions, LA pieces ahead, in registers (thread: positions 64*(2j+u) + tid/4, u < 2, columns
+// c .. c+3); the products of piece j+1 are staged into one of two LDS buffers while the chain lanes
+// add piece j from the other, one barrier per piece.
+#define QMH_PV_LONG 8192
+template <int LA>
+__device__ __forceinline__ void pv_mha_long(const float *__restrict__ s0, const float *__restrict__ V,
+                                            float *__restrict__ out, int n, int h, int kvh, int i0, int hd, int kvd,
+                                            float *P, float *Vs2) {
+    constexpr int PC = 128, VS = PC + 4;  // positions per piece; staged row stride (4 mod 64 floats)
+    static_assert(PC * QMH_PV_CW / 4 == 2 * QMH_WG, "a piece is two float4 loads of every thread");
+    __shared__ float wmax[QMH_WG / 64];
+    __shared__ double wsum[QMH_WG / 64];
+    __shared__ double ser_s;
+    __shared__ uint64_t etab[32];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
+    const float *vcol = V + (size_t)kvh * hd + cc;
+    const int npc = (n + PC - 1) / PC;
+    float4 vr[LA + 1][2];  // ring of V pieces: piece j in vr[j % (LA + 1)]
+    auto vload = [&](int j, float4(&d)[2]) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int t = (2 * j + u) * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
+            d[u] = *(const float4 *)(vcol + (size_t)tcl * kvd);
+        }
+    };
+    // the first pieces' V, issued before the statistics so they arrive under them
+#pragma unroll
+    for (int k = 0; k < LA; k++) vload(k < npc ? k : npc - 1, vr[k]);
+    const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
+    // softmax statistics (src/ops.c:100-112) as k_attn_pv_mha: max (NaN never wins; a NaN at x[0]
+    // stays), e_t = expf(x_t - max) kept in P, the double sum as a tree checked against the serial order
+    float m = -__builtin_inff();
+    for (int t = tid; t < n; t += QMH_WG) {
+        const float x = s0[t];
+        m = x > m ? x : m;
+    }
+    m = qmh_wave_max(m);
+    if (lane == 0) wmax[wv] = m;
+    if (tid < 32) etab[tid] = etv;
+    __syncthreads();
+    m = wmax[0];
+#pragma unroll
+    for (int w = 1; w < QMH_WG / 64; w++) m = fmaxf(m, wmax[w]);
+    if (s0[0] != s0[0]) m = s0[0];
+    double sum = 0.0;
+    for (int t = tid; t < n; t += QMH_WG) {
+        const float e = qmh_expf_t(s0[t] - m, etab);
+        P[t] = e;
+        sum += (double)e;
+    }
+    sum = qmh_wave_sum_d(sum);
+    if (lane == 0) wsum[wv] = sum;
+    __syncthreads();  // also publishes P
+    sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < QMH_WG / 64; w++) sum += wsum[w];
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform: the reference's serial order
+        if (tid == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)P[t];
+            ser_s = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(ser_s);
+    }
+    // products of piece j into buffer b: p_t * v_t, +0 past n (the chain's sum started at +0 and
+    // is never -0, so the padding changes nothing)
+    auto stage = [&](int j, const float4(&v2)[2], int b) {
+        float *buf = Vs2 + (size_t)b * QMH_PV_CW * VS;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int tl = u * (QMH_WG / 4) + (tid >> 2), t = j * PC + tl;
+            const bool on = t < n;
+            const float p = on ? P[t] * inv : 0.0f;
+            const float4 v = v2[u];
+            float *dst = buf + (size_t)(4 * (tid & 3)) * VS + tl;
+            dst[0] = on ? p * v.x : 0.0f;
+            dst[VS] = on ? p * v.y : 0.0f;
+            dst[2 * VS] = on ? p * v.z : 0.0f;
+            dst[3 * VS] = on ? p * v.w : 0.0f;
+        }
+    };
+    const bool chain = tid < QMH_PV_CW;
+    float acc = 0.0f;
+    stage(0, vr[0], 0);
+    __syncthreads();
+    // piece j: load piece j+LA, stage piece j+1, chain piece j, barrier. Unrolled by LA+1 so the
+    // ring indices are constants.
+    // Loads and staging are unconditional (a piece past the end stages zeros into the buffer no chain
+    // reads next), and the barrier waits only for LDS: the V loads of the next LA pieces stay in flight.
+    auto piece = [&](int j, int r) {  // r = j % (LA + 1)
+        vload(j + LA < npc ? j + LA : npc - 1, vr[(r + LA) % (LA + 1)]);
+        stage(j + 1, vr[(r + 1) % (LA + 1)], (j + 1) & 1);
+        if (chain) {
+            // out = out + p_t*v_t in t order; the piece's terms read at once, then added
+            const float4 *v4 = (const float4 *)(Vs2 + (size_t)(j & 1) * QMH_PV_CW * VS + (size_t)tid * VS);
+            float4 vc[PC / 4];
+#pragma unroll
+            for (int q = 0; q < PC / 4; q++) vc[q] = v4[q];
+#pragma unroll
+            for (int q = 0; q < PC / 4; q++) {
+                acc = acc + vc[q].x;
+                acc = acc + vc[q].y;
+                acc = acc + vc[q].z;
+                acc = acc + vc[q].w;
+            }
+        }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    int j0 = 0;
+    for (; j0 + LA + 1 <= npc; j0 += LA + 1) {
+#pragma unroll
+        for (int r = 0; r <= LA; r++) piece(j0 + r, r);
+    }
+#pragma unroll
+    for (int r = 0; r < LA; r++)
+        if (j0 + r < npc) piece(j0 + r, r);  // uniform
+    if (chain && i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
+}
+
+// One workgroup per (query head, 16 output columns), head_dim a multiple of 4: its V is that of the
+// head's kv head h / (n_heads / n_kv) (the query heads of a group read it from L2). Contexts of up
+// to TC positions run here; up to QMH_PV_LONG, pv_mha_long; longer ones, only when every kv head
+// serves one query head (the launcher keeps grouped heads within QMH_PV_LONG), attn_pv_chunks. Same
+// sums in the same order as the reference, laid out for a shorter critical path:
 //   * V is read as float4 (4 columns of one position per thread);
 //   * the softmax exponentials e_t stay in LDS (P) from the statistics to the products, and the
 //     serial fallback of the sum reads them there;
@@ -266,7 +393,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv(const float *__restrict__ at
 template <int TC>
 __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict__ att, const float *__restrict__ V,
                                                         float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
-                                                        int hd, int max_seq) {
+                                                        int n_kv, int hd, int max_seq) {
     constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
     constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
     constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
@@ -282,12 +409,18 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     __shared__ uint64_t etab[32];
     const int n = *pos_ptr + 1;
     if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
-    if (n > TC) {
+    if (n > QMH_PV_LONG) {
+        if (n_kv != n_heads) return;  // grouped heads never get here (the launcher's bound on max_seq)
         attn_pv_chunks<TC, true>(att, V, out, n, n_heads, n_heads, hd, max_seq);
         return;
     }
+    if (n > TC) {
+        pv_mha_long<3>(att + (size_t)blockIdx.x * max_seq, V, out, n, blockIdx.x, blockIdx.x / (n_heads / n_kv),
+                       blockIdx.y * QMH_PV_CW, hd, hd * n_kv, pv_smem, pv_smem + QMH_PV_LONG);
+        return;
+    }
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int h = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_heads;
+    const int h = blockIdx.x, kvh = h / (n_heads / n_kv), i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
     const float *s0 = att + (size_t)h * max_seq;
     // loads: expf's table (oldest, so storing it to LDS below waits for nothing else), the head's
     // scores, then the V float4s (position k*64 + tid/4, columns c .. c+3; columns past hd
@@ -304,7 +437,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
 #pragma unroll
     for (int k = 0; k < L4; k++) {
         const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
-        vv[k] = *(const float4 *)(V + (size_t)tcl * kvd + (size_t)h * hd + cc);
+        vv[k] = *(const float4 *)(V + (size_t)tcl * kvd + (size_t)kvh * hd + cc);
     }
     // softmax statistics (src/ops.c:100-112): max (NaN never wins; a NaN at x[0] stays),
     // e_t = expf(x_t - max) kept in P, the double sum as a tree checked against the serial order
@@ -405,10 +538,15 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *
 #define QMH_PV_GO(TC, MHA)                                                                                \
     hipLaunchKernelGGL((k_attn_pv<TC, MHA>), grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
                        s, att, vcache, out, pos_ptr, n_heads, n_kv_heads, head_dim, max_seq)
-    if (group == 1 && head_dim % 4 == 0)
-        hipLaunchKernelGGL(k_attn_pv_mha<640>, grid, dim3(QMH_WG),
-                           sizeof(float) * ((size_t)640 + QMH_PV_CW * (640 + 4)), s, att, vcache, out, pos_ptr, n_heads,
-                           head_dim, max_seq);
+    if (head_dim % 4 == 0 && (group == 1 || max_seq <= QMH_PV_LONG)) {
+        // one workgroup per query head; the larger of the two paths' LDS: the whole-context one
+        // (<= 640 positions) and the streamed one (exponentials of up to QMH_PV_LONG positions, two
+        // staged pieces of 128)
+        const size_t lds_a = (size_t)640 + QMH_PV_CW * (640 + 4), lds_b = (size_t)QMH_PV_LONG + 2 * QMH_PV_CW * (128 + 4);
+        hipLaunchKernelGGL(k_attn_pv_mha<640>, dim3(n_heads, grid.y), dim3(QMH_WG),
+                           sizeof(float) * (lds_a > lds_b ? lds_a : lds_b), s, att, vcache, out, pos_ptr, n_heads,
+                           n_kv_heads, head_dim, max_seq);
+    }
     else if (group == 1) QMH_PV_GO(640, true);
     else if (group <= 8) QMH_PV_GO(640, false);
     else QMH_PV_GO(256, false);

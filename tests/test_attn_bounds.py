@@ -9,11 +9,14 @@ passes. The formulas restate the kernels' own index arithmetic, line by line:
   * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:24-61 (launcher :63-89)
   * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:368-396 (launcher :399-415): clamped float4 K
                           loads past the last position (t <= max_seq-4)
-  * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:92-246 (k_attn_pv :249-256): unconditional V
+  * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:92-246 (k_attn_pv :249-255): unconditional V
                           and score loads clamped to position n-1 / score 0, columns to head_dim-1
-  * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:267-397: float4 V loads clamped to position
-                          n-1 and column head_dim-4, pieces of 128 staged products
-  * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:399-417: kernel choice and dynamic LDS
+  * pv_mha_long<LA>       quillm_amd/csrc/qmh_attn.hip:262-380: exponentials of up to 8192 positions,
+                          V pieces of 128 positions loaded LA pieces ahead (clamped to the last piece
+                          and position n-1), two staged buffers
+  * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:393-530: one workgroup per query head, float4 V
+                          loads of its kv head clamped to position n-1 and column head_dim-4
+  * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:532-555: kernel choice and dynamic LDS
 This is a model: a kernel edit that changes an index must change it here too.
 """
 import numpy as np
@@ -26,9 +29,10 @@ SHAPES = [
     (6, 6, 48, 256), (6, 2, 48, 256), (12, 12, 64, 1024), (32, 4, 64, 2048), (32, 32, 128, 4096),
     (4, 2, 16, 64), (6, 3, 12, 64), (3, 3, 32, 48), (12, 1, 8, 300), (4, 2, 48, 136),
     (2, 2, 128, 1300), (6, 6, 10, 700), (4, 2, 32, 700), (32, 32, 128, 640),
+    (4, 2, 16, 9000), (2, 2, 16, 9000), (8, 1, 12, 8192), (4, 4, 64, 8193),
 ]
 POSITIONS = [0, 1, 2, 3, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 575, 639, 640, 641, 700,
-             767, 768, 1023, 1024, 1279, 1280, 1281, 2047, 4095]
+             767, 768, 1023, 1024, 1279, 1280, 1281, 2047, 4095, 8191, 8192, 8193, 8900]
 
 
 def positions(S):
@@ -120,11 +124,12 @@ def pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats):
     inb("pv out", outi[np.broadcast_to(ok[None], outi.shape)], ext.out)
 
 
-def pv_mha(TC, nh, hd, S, n, ext, lds_floats):
-    """k_attn_pv_mha<TC> for n <= TC (longer contexts take attn_pv_chunks<TC, true>)."""
-    kvd = hd * nh
+def pv_mha(TC, nh, nkv, hd, S, n, ext, lds_floats):
+    """k_attn_pv_mha<TC> for n <= TC over grid (nh, ceil(hd/16)) x 256 threads."""
+    kvd = hd * nkv
     tid = np.arange(WG)
     h = np.arange(nh)
+    kvh = h // (nh // nkv)
     i0 = np.arange(0, hd, CW)
     SK = (TC + WG - 1) // WG
     t = tid[None, :] + WG * np.arange(SK)[:, None]
@@ -135,7 +140,7 @@ def pv_mha(TC, nh, hd, S, n, ext, lds_floats):
     tv = np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :]
     tcl = np.minimum(tv, n - 1)
     for r in range(4):  # the float4's four floats
-        inb("mha V", tcl[None, None, :, :] * kvd + h[:, None, None, None] * hd + cc[None, :, None, :] + r, ext.V)
+        inb("mha V", tcl[None, None, :, :] * kvd + kvh[:, None, None, None] * hd + cc[None, :, None, :] + r, ext.V)
     inb("mha P", np.arange(n), TC)
     PC = 128
     npc = (n + PC - 1) // PC
@@ -149,9 +154,55 @@ def pv_mha(TC, nh, hd, S, n, ext, lds_floats):
         inb("mha chain", TC + np.arange(CW)[:, None] * (TC + 4) + 4 * (j * (PC // 4) + q)[None, :] + 3, lds_floats)
     # float4 staging rows and chain rows stay 16-byte aligned
     assert (TC % 4, (TC + 4) % 4) == (0, 0)
+    mha_out(nh, hd, ext)
+
+
+def mha_out(nh, hd, ext):
+    h, i0 = np.arange(nh), np.arange(0, hd, CW)
     ok = (i0[:, None] + np.arange(CW)[None, :]) < hd
     outi = h[:, None, None] * hd + i0[None, :, None] + np.arange(CW)[None, None, :]
     inb("mha out", outi[np.broadcast_to(ok[None], outi.shape)], ext.out)
+
+
+PV_LONG, LA = 8192, 3
+
+
+def pv_mha_long(nh, nkv, hd, S, n, ext, lds_floats):
+    """pv_mha_long<3> for TC < n <= 8192, called by k_attn_pv_mha with P at LDS float 0 and the two
+    staged buffers at float 8192."""
+    kvd = hd * nkv
+    tid = np.arange(WG)
+    h = np.arange(nh)
+    kvh = h // (nh // nkv)
+    i0 = np.arange(0, hd, CW)
+    PC, VS = 128, 132
+    npc = (n + PC - 1) // PC
+    c = i0[:, None] + 4 * (tid & 3)[None, :]
+    cc = np.where(c <= hd - 4, c, hd - 4)
+    # every piece index vload is given: the first LA (clamped to npc-1), then j+LA clamped
+    js = sorted({min(k, npc - 1) for k in range(LA)} | {min(j + LA, npc - 1) for j in range(npc + LA)})
+    for j in js:
+        for u in range(2):
+            t = (2 * j + u) * (WG // 4) + (tid >> 2)
+            tcl = np.minimum(t, n - 1)
+            for r in range(4):
+                inb("long V", tcl[None, None, :] * kvd + (kvh[:, None] * hd)[:, :, None] + cc[None, :, :] + r, ext.V)
+    inb("long scores", h[:, None] * S + np.arange(n)[None, :], ext.att)
+    inb("long P", np.arange(n), PV_LONG)
+    # staging of pieces 0 .. npc (the last piece's successor stages zeros); reads of P only below n
+    for j in range(npc + 1):
+        b = j & 1
+        for u in range(2):
+            tl = u * (WG // 4) + (tid >> 2)
+            t = j * PC + tl
+            inb("long P stage", t[t < n], PV_LONG)
+            for r in range(4):
+                inb("long stage", PV_LONG + b * CW * VS + (4 * (tid & 3) + r) * VS + tl, lds_floats)
+    for j in range(npc):
+        inb("long chain", PV_LONG + (j & 1) * CW * VS + np.arange(CW)[:, None] * VS + 4 * np.arange(PC // 4)[None, :] + 3,
+            lds_floats)
+    assert VS % 4 == 0 and PV_LONG % 4 == 0
+    mha_out(nh, hd, ext)
 
 
 LDS_MAX = 160 * 1024 - 1024  # per workgroup on gfx950, less the kernels' static LDS
@@ -162,12 +213,15 @@ def pv(nh, nkv, hd, S, pos, ext):
     group = nh // nkv
     assert group <= 16 and group * CW <= WG
     n = pos + 1
-    if group == 1 and hd % 4 == 0:
-        lds_floats = 640 + CW * (640 + 4)
+    if hd % 4 == 0 and (group == 1 or S <= PV_LONG):
+        lds_floats = max(640 + CW * (640 + 4), PV_LONG + 2 * CW * (128 + 4))
         assert 4 * lds_floats <= LDS_MAX
         if n <= 640:
-            pv_mha(640, nh, hd, S, n, ext, lds_floats)
+            pv_mha(640, nh, nkv, hd, S, n, ext, lds_floats)
+        elif n <= PV_LONG:
+            pv_mha_long(nh, nkv, hd, S, n, ext, lds_floats)
         else:
+            assert group == 1  # the kernel's chunked fallback is for one query head per kv head
             pv_chunks(640, True, nh, nh, hd, S, n, ext, lds_floats)
         return
     TC, MHA = (640, True) if group == 1 else (640, False) if group <= 8 else (256, False)
@@ -195,3 +249,13 @@ def test_model_catches_an_out_of_range_clamp():
     inb("kept clamp", (nkv - 1) * hd * S + (hd - 1) * S + np.minimum(t, S - 4) + 3, K)
     with pytest.raises(AssertionError):
         inb("planted clamp", (nkv - 1) * hd * S + (hd - 1) * S + np.minimum(t, S - 1) + 3, K)
+
+
+def test_model_catches_a_wrong_kv_head():
+    """Grouped heads read V of kv head h // group with row stride head_dim * n_kv: taking the query
+    head's index and stride instead runs past the cache."""
+    nh, nkv, hd, S = 4, 2, 16, 700
+    ext = Extents(nh, nkv, hd, S)
+    pv_mha_long(nh, nkv, hd, S, S, ext, PV_LONG + 2 * CW * 132)
+    with pytest.raises(AssertionError):
+        pv_mha_long(nh, nh, hd, S, S, ext, PV_LONG + 2 * CW * 132)

@@ -160,6 +160,12 @@ def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
     # (positions 638-642 cross into the second chunk, 1279-1281 into the third)
     ("mha128", dict(dim=256, hidden_dim=320, n_layers=1, n_heads=2, n_kv_heads=2, vocab_size=300, max_seq=1300),
      "q4_0", [(636, 646), (1277, 1286)]),
+    # grouped heads (2 and 8 query heads per kv head), head_dim 32 and 16: the per-query-head P.V
+    # kernel reading its kv head's V, whole-context and streamed past 640 positions
+    ("gqa32", dict(dim=128, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=1300),
+     "q8_0", [(636, 646), (1277, 1286)]),
+    ("gqa8x16", dict(dim=128, hidden_dim=256, n_layers=1, n_heads=8, n_kv_heads=1, vocab_size=300, max_seq=900),
+     "q4_0", [(636, 646), (890, 900)]),
     # head_dim 10 (not a multiple of 4): the scalar-column decode attention, and prompts that run as
     # sequential forwards (the batched prompt path takes head_dim % 4 == 0 only)
     ("mha10", dict(dim=60, hidden_dim=128, n_layers=1, n_heads=6, n_kv_heads=6, vocab_size=300, max_seq=700),
