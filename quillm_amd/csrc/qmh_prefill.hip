@@ -24,6 +24,8 @@
 #define QMH_Q4 3
 
 typedef int pf_v4i __attribute__((ext_vector_type(4)));
+typedef float pf_v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 pf_v4h __attribute__((ext_vector_type(4)));
 
 // ============================================================================ embedding
 
@@ -207,7 +209,8 @@ __device__ __forceinline__ uint32_t pf_slot0(const qmh_pf_args &a, int row, int 
 template <int NM, int NR, int TW>
 struct PfBlock {
     long A[NM][NR];   // raw weight codes: 8 int8 (Q8_0) or 4 nibble bytes (Q4_0, low word)
-    uint2 sc[NM][NR];
+    uint2 sc[NM][NR]; // the fp16 scales of the lane's 4 D rows (k_sk_gemm)
+    uint32_t wh[NM][NR];  // the fp16 scale of the lane's A row (k_pf_gemm)
     long B[TW];
     float dx[TW];
 };
@@ -219,12 +222,15 @@ struct PfBlock {
 template <int NM, int NR>
 struct PfLane {
     uint32_t a[NM][NR], s[NM][NR];  // weight codes (bytes), scales (elements) at block 0
+    uint32_t w[NM][NR];             // k_pf_gemm: the scale (element) of the lane's A row at block 0
     uint32_t x, d;                  // activation codes (bytes), scales (elements) of token tile 0
 };
 
 // Loads only: no value is used here, so the wait for these loads falls where the block is
 // multiplied, PD blocks later.
-template <int WT, int NM, int NR, int TW>
+// PM: the scales as k_pf_gemm takes them (one per A row, for the scale MFMA), else the 4 of the
+// lane's D rows.
+template <int WT, int NM, int NR, int TW, bool PM = false>
 __device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLane<NM, NR> &ln,
                                         PfBlock<NM, NR, TW> &o) {
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;
@@ -236,7 +242,8 @@ __device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLan
         for (int r = 0; r < NR; r++) {
             if (WT == QMH_Q8) o.A[m][r] = *(const long *)(cb + ln.a[m][r]);
             else o.A[m][r] = (long)*(const uint32_t *)(cb + ln.a[m][r]);
-            o.sc[m][r] = *(const uint2 *)(sb + ln.s[m][r]);
+            if (PM) o.wh[m][r] = sb[ln.w[m][r]];
+            else o.sc[m][r] = *(const uint2 *)(sb + ln.s[m][r]);
         }
     const int8_t *xb = a.xc + (size_t)b * a.PP * 32;
     const float *db = a.xd + (size_t)b * a.PP;
@@ -247,34 +254,48 @@ __device__ __forceinline__ void pf_load(const qmh_pf_args &a, int b, const PfLan
     }
 }
 
-// one block into the chains: s = s + (float)acc * (dw * dx) per (row, token) pair. The MFMAs of
-// row tile q+1 (each into its own registers) are issued before the epilogue of row tile q, so the
-// multiplies run under the float work instead of each waiting for the previous results to be
-// consumed. Every accumulator's chain stays in block order.
+// one block into the chains: s = s + (float)acc * (dw * dx) per (row, token) pair. Two MFMAs per
+// (row tile, token tile): the block's exact int32 dots, and the scale products dw * dx as the outer
+// product of the row tile's 16 fp16 scales and the token tile's 16 (k = 0 of an f16 MFMA; every
+// other k is 0 * 0). The product of two fp16 values is exact in fp32, so the MFMA returns the
+// reference's dw * dx bit for bit (but +0 for -0: the chain starts at +0 and never holds -0, so
+// s + (+0) == s + (-0) and the term's zero sign changes nothing); the VALU keeps the conversion,
+// the multiply and the add, in the reference's order. k0 is 0xffff in the lanes of k = 0..3
+// (lane / 16 == 0), else 0.
+// The MFMAs of the next (row tile, token tile) pair go out, into their own registers, before the
+// terms of the current one, so the multiplies run under the float work instead of each waiting for
+// the previous results to be consumed. Every accumulator's chain stays in block order.
 template <int WT, int NM, int NR, int TW>
-__device__ __forceinline__ void pf_mul(const PfBlock<NM, NR, TW> &cur, float (&s)[NM][NR][TW][4]) {
-    constexpr int Q = NM * NR;  // row tiles (m, r) = (q / NR, q % NR)
-    pf_v4i acc[2][TW];
-    auto issue = [&](int q, pf_v4i(&d)[TW]) {
-        const long Am = WT == QMH_Q8 ? cur.A[q / NR][q % NR] : pf_q4_operand((uint32_t)cur.A[q / NR][q % NR]);
+__device__ __forceinline__ void pf_mul(const PfBlock<NM, NR, TW> &cur, float (&s)[NM][NR][TW][4], uint32_t k0) {
+    constexpr int Q = NM * NR, U = Q * TW;  // pair u: row tile (m, r) = (q / NR, q % NR), q = u / TW; tt = u % TW
+    pf_v4h Bs[TW];                          // token tile tt's scales at k = 0
 #pragma unroll
-        for (int tt = 0; tt < TW; tt++) {
-            const pf_v4i z = {0, 0, 0, 0};
-            d[tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, cur.B[tt], z, 0, 0, 0);
-        }
-    };
-    issue(0, acc[0]);
+    for (int tt = 0; tt < TW; tt++) {
+        const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)cur.dx[tt]) & k0;  // exact: dx is fp16
+        Bs[tt] = __builtin_bit_cast(pf_v4h, make_uint2(h, 0u));
+    }
+    long Am[Q];
+    pf_v4h As[Q];  // row tile q's scales at k = 0
 #pragma unroll
     for (int q = 0; q < Q; q++) {
-        if (q + 1 < Q) issue(q + 1, acc[(q + 1) & 1]);
-        const int m = q / NR, r = q % NR;
-        const float dw[4] = {qmh_h2f((uint16_t)(cur.sc[m][r].x & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].x >> 16)),
-                             qmh_h2f((uint16_t)(cur.sc[m][r].y & 0xffffu)), qmh_h2f((uint16_t)(cur.sc[m][r].y >> 16))};
+        Am[q] = WT == QMH_Q8 ? cur.A[q / NR][q % NR] : pf_q4_operand((uint32_t)cur.A[q / NR][q % NR]);
+        As[q] = __builtin_bit_cast(pf_v4h, make_uint2(cur.wh[q / NR][q % NR] & k0, 0u));
+    }
+    pf_v4i acc[2];
+    pf_v4f pw[2];
+    auto issue = [&](int u, pf_v4i &d, pf_v4f &pd) {
+        const pf_v4i z = {0, 0, 0, 0};
+        const pf_v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am[u / TW], cur.B[u % TW], z, 0, 0, 0);
+        pd = __builtin_amdgcn_mfma_f32_16x16x16f16(As[u / TW], Bs[u % TW], zf, 0, 0, 0);
+    };
+    issue(0, acc[0], pw[0]);
 #pragma unroll
-        for (int tt = 0; tt < TW; tt++)
+    for (int u = 0; u < U; u++) {
+        if (u + 1 < U) issue(u + 1, acc[(u + 1) & 1], pw[(u + 1) & 1]);
+        const int q = u / TW, m = q / NR, r = q % NR, tt = u % TW;
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                s[m][r][tt][e] = s[m][r][tt][e] + (float)acc[q & 1][tt][e] * (dw[e] * cur.dx[tt]);
+        for (int e = 0; e < 4; e++) s[m][r][tt][e] = s[m][r][tt][e] + (float)acc[u & 1][e] * pw[u & 1][e];
     }
 }
 
@@ -313,15 +334,16 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
     PfLane<NM, NR> ln;
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-        const int row = r0 + 16 * r + (l & 15), grp = r0 + 16 * r + 4 * kq;  // A row; first D row
+        const int row = r0 + 16 * r + (l & 15);  // the lane's A row
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             ln.a[m][r] = pf_slot0(a, row < a.rows_alloc ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
-            ln.s[m][r] = pf_slot0(a, grp < a.rows_alloc ? grp : 0, m);
+            ln.w[m][r] = pf_slot0(a, row < a.rows_alloc ? row : 0, m);
         }
     }
     ln.x = (uint32_t)(t0 + (l & 15)) * 32 + 8 * kq;
     ln.d = (uint32_t)(t0 + (l & 15));
+    const uint32_t k0 = kq == 0 ? 0xffffu : 0u;
     float s[NM][NR][TW][4];
 #pragma unroll
     for (int m = 0; m < NM; m++)
@@ -337,19 +359,19 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
     // block b0: ring[j] holds block b0 + j, j < PD.
     PfBlock<NM, NR, TW> ring[PD + 1];
 #pragma unroll
-    for (int j = 0; j < PD; j++) pf_load<WT, NM, NR, TW>(a, j < a.nb ? j : a.nb - 1, ln, ring[j]);
+    for (int j = 0; j < PD; j++) pf_load<WT, NM, NR, TW, true>(a, j < a.nb ? j : a.nb - 1, ln, ring[j]);
     int b0 = 0;
     for (; b0 + PD < a.nb; b0 += PD + 1) {
 #pragma unroll
         for (int j = 0; j <= PD; j++) {
             const int bn = b0 + j + PD;
-            pf_load<WT, NM, NR, TW>(a, bn < a.nb ? bn : a.nb - 1, ln, ring[(j + PD) % (PD + 1)]);
-            pf_mul<WT, NM, NR, TW>(ring[j], s);
+            pf_load<WT, NM, NR, TW, true>(a, bn < a.nb ? bn : a.nb - 1, ln, ring[(j + PD) % (PD + 1)]);
+            pf_mul<WT, NM, NR, TW>(ring[j], s, k0);
         }
     }
 #pragma unroll
     for (int j = 0; j < PD; j++)
-        if (b0 + j < a.nb) pf_mul<WT, NM, NR, TW>(ring[j], s);
+        if (b0 + j < a.nb) pf_mul<WT, NM, NR, TW>(ring[j], s, k0);
     // epilogues: lane l holds rows r0 + 16*r + 4*kq + e (e < 4) of tokens t0 + 16*tt + l%16
 #pragma unroll
     for (int r = 0; r < NR; r++)
