@@ -66,12 +66,13 @@ def prefill_flops(w, P, logits_rows):
 
 
 def prefill_valu_floor_s(w, P, logits_rows):
-    """The bitwise matmul epilogue's VALU floor: 4 operations (cvt, mul, mul, add) per (row, token,
-    block) in the reference's order, at the device's fp32 VALU rate."""
+    """The bitwise matmul epilogue's VALU floor: 3 operations (cvt, mul, add) per (row, token, block) in
+    the reference's order (the scale product dw*dx, exact, comes from an f16 MFMA), at the device's fp32
+    VALU rate."""
     D, H, L, V, kvd = w.dim, w.hidden_dim, w.n_layers, w.vocab_size, w.kvd
     nb = lambda n: (n + 31) // 32
     rows_nb = L * ((2 * D + 2 * kvd) * nb(D) + 2 * H * nb(D) + D * nb(H))
-    return 4 * (P * rows_nb + logits_rows * V * nb(D)) / VALU_LANE_OPS
+    return 3 * (P * rows_nb + logits_rows * V * nb(D)) / VALU_LANE_OPS
 
 
 def pmc_traffic(name):
@@ -204,8 +205,9 @@ def measure(q, w, P, K, W, detail=False):
                 "frac": round(ach / 1e12 / INT8_PEAK_TOPS, 4), "flops": int(flops),
                 "frac_of_fp32_mfma": round(ach / 1e12 / FP32_MFMA_PEAK_TFS, 4),
                 "valu_floor_ms": round(prefill_valu_floor_s(w, P, P) * 1e3, 3),
-                "note": "int8 MFMA block dots (exact) + the bitwise f32 epilogue on the VALU (4 ops per row, token, "
-                        "block); flops counted as the reference's P forwards, every position's logits included",
+                "note": "int8 MFMA block dots and f16 MFMA scale products (both exact) + the bitwise f32 epilogue "
+                        "on the VALU (3 ops per row, token, block); flops counted as the reference's P forwards, "
+                        "every position's logits included",
             }
             # the same steps sampled on the device with the reference CLI's default sampler
             # (src/main.c:70-72: temperature 0.8, top-k 0, top-p 0.95, seed 42); wall clock, synchronous
