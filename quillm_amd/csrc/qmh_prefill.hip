@@ -79,19 +79,17 @@ __device__ __forceinline__ void pf_quant_block(const float (&v)[4], int b, int n
     const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
     int q[4];
     qmh_q8_codes4(v, dd, qmh_rcp(dd), q);
+    const uint32_t b0 = (uint32_t)q[0] & 0xffu, b1 = (uint32_t)q[1] & 0xffu, b2 = (uint32_t)q[2] & 0xffu,
+                   b3 = (uint32_t)q[3] & 0xffu;
+    // one dword per lane: bytes 4*sub .. +3 of the block. perm8 (elements 8g+e, e = 0..7, at
+    // 8g + {0,4,1,5,2,6,3,7}[e]): the lane pair of a group (elements 0-3, 4-7) swaps half-words,
+    // {e0 e2 | e1 e3} against {e4 e6 | e5 e7}, and writes {e0 e2 e4 e6} (even lane) or {e1 e3 e5 e7}.
+    const uint32_t pk = b0 | (b2 << 8) | (b1 << 16) | (b3 << 24);
+    const uint32_t pp = (uint32_t)qmh_dpp<QMH_DPP_QXOR1>((int)pk);  // every lane of the block is active here
+    const uint32_t w = !perm8 ? (b0 | (b1 << 8) | (b2 << 16) | (b3 << 24))
+                       : (sub & 1) == 0 ? ((pk & 0xffffu) | (pp << 16)) : ((pp >> 16) | (pk & 0xffff0000u));
     if (b < nb) {
-        int8_t *c = xc + ((size_t)b * PP + p) * 32;
-        if (perm8) {  // elements 8g+e (e = 0..7) at 8g + {0,4,1,5,2,6,3,7}[e]
-            const int g = sub >> 1, e0 = (sub & 1) * 4;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int e = e0 + j;
-                c[8 * g + ((e & 1) ? 4 + (e >> 1) : (e >> 1))] = (int8_t)q[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) c[sub * 4 + j] = (int8_t)q[j];
-        }
+        *(uint32_t *)(xc + ((size_t)b * PP + p) * 32 + 4 * sub) = w;
         if (sub == 0) xd[(size_t)b * PP + p] = dd;
     }
 }
