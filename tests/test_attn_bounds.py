@@ -6,8 +6,8 @@ the test models) and positions on both sides of each chunk boundary, and checked
 extent of its buffer: the per-layer caches K [kvd][max_seq] and V [max_seq][kvd], the scores
 att [n_heads][max_seq], q and out [n_heads*head_dim], and the dynamic LDS bytes the launcher
 passes. The formulas restate the kernels' own index arithmetic, line by line:
-  * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:24-61 (launcher :63-89)
-  * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:368-396 (launcher :399-415): clamped float4 K
+  * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:24-61 (launcher :63-81)
+  * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:368-400 (launcher :402-416): clamped float4 K
                           loads past the last position (t <= max_seq-4)
   * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:92-246 (k_attn_pv :249-255): unconditional V
                           and score loads clamped to position n-1 / score 0, columns to head_dim-1
