@@ -102,6 +102,12 @@ typedef struct {
     float eps;
     /* epilogue: out0 row-major [P][ld0]; QKV: q -> out0, k -> out1 ([kvd][max_seq]), v -> out2 */
     int epi;
+    /* SWIGLU through the tiled matmul (P > 32): with qxc set, the output is written only as the next
+     * matmul's Q8_0 image, codes [nb][PP][32] (Q4_0 order when qperm8) and scales [nb][PP], instead of
+     * out0 (the quantization the launcher would run on it, bit for bit) */
+    int8_t *qxc;
+    float *qxd;
+    int qperm8;
     float *out0, *out1, *out2;
     int ld0, seg1, seg2;
     const float *rope;

@@ -371,6 +371,50 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
     for (int j = 0; j < PD; j++)
         if (b0 + j < a.nb) pf_mul<WT, NM, NR, TW>(ring[j], s, k0);
     // epilogues: lane l holds rows r0 + 16*r + 4*kq + e (e < 4) of tokens t0 + 16*tt + l%16
+    if (NR == 2 && a.epi == QMH_PF_SWIGLU && a.qxc) {  // uniform
+        // W2's input as its Q8_0 image: the wave's 32 rows (r0 % 32 == 0) are block r0/32 of each of
+        // its tokens; lanes l, l^16, l^32, l^48 hold a token's 32 values (8 each: elements
+        // 16*r + 4*kq + e). The same steps as k_pf_quant's block (src/quant.c:27-52): amax, the fp16
+        // scale, the codes; rows past `rows` are 0 there and here.
+        const int b = r0 >> 5;
+#pragma unroll
+        for (int tt = 0; tt < TW; tt++) {
+            const int p = t0 + 16 * tt + (l & 15);
+            float v[NR][4], m = 0.0f;
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int row = r0 + 16 * r + 4 * kq + e;
+                    const float y = s[0][r][tt][e], up = s[NM - 1][r][tt][e];
+                    v[r][e] = row < a.rows ? y / (1.0f + qmh_expf(-y)) * up : 0.0f;  // silu(g)*u (src/ops.c:128-133)
+                    const float av = fabsf(v[r][e]);
+                    m = av > m ? av : m;
+                }
+            float o = __shfl_xor(m, 16);
+            m = o > m ? o : m;
+            o = __shfl_xor(m, 32);
+            m = o > m ? o : m;
+            const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
+            const float rinv = qmh_rcp(dd);
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                int q[4];
+                qmh_q8_codes4(v[r], dd, rinv, q);
+                const uint32_t b0 = (uint32_t)q[0] & 0xffu, b1 = (uint32_t)q[1] & 0xffu, b2 = (uint32_t)q[2] & 0xffu,
+                               b3 = (uint32_t)q[3] & 0xffu;
+                // bytes 16*r + 4*kq .. +3 of the block; the Q4_0 order (8g+e at 8g + {0,4,1,5,2,6,3,7}[e])
+                // by a half-word swap with lane l^16, as in k_pf_quant
+                const uint32_t pk = b0 | (b2 << 8) | (b1 << 16) | (b3 << 24);
+                const uint32_t pp = (uint32_t)__shfl_xor((int)pk, 16);
+                const uint32_t w = !a.qperm8 ? (b0 | (b1 << 8) | (b2 << 16) | (b3 << 24))
+                                   : (kq & 1) == 0 ? ((pk & 0xffffu) | (pp << 16)) : ((pp >> 16) | (pk & 0xffff0000u));
+                if (p < a.P) *(uint32_t *)(a.qxc + ((size_t)b * a.PP + p) * 32 + 16 * r + 4 * kq) = w;
+            }
+            if (p < a.P && kq == 0) a.qxd[(size_t)b * a.PP + p] = dd;
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < NR; r++)
 #pragma unroll
@@ -741,6 +785,8 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
+    // the image output exists only in the tiled matmul's SwiGLU epilogue (more than 32 tokens)
+    if (a->qxc && (a->epi != QMH_PF_SWIGLU || !a->qxd || a->P <= 32 || PF_NR != 2)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     if (a->xf && (a->nxf < 1 || a->nxf > 32 * a->nb || a->ldxf < a->nxf)) return (int)hipErrorInvalidValue;
     // the multi-token matvec when one tile's terms fit its LDS with the records. It quantizes a plain

@@ -390,6 +390,8 @@ struct qmh_model {
     int pf_ok, pf_cap, pf_pp;
     int32_t *d_pf_tok, *h_pf_tok;
     float *d_pf_x, *d_pf_xb, *d_pf_q, *d_pf_hb, *d_pf_att, *d_pf_logits, *d_pf_xd;
+    int8_t *d_pf_xc2; /* W2's input image, written by W1|W3's epilogue past 32 tokens */
+    float *d_pf_xd2;
     int8_t *d_pf_xc;
 };
 
@@ -598,7 +600,7 @@ void qmh_model_free(qmh_model *m) {
     void *dev[] = {m->d_embd,   m->d_norms,  m->d_rope,     m->d_x,    m->d_xb,   m->d_q,     m->d_hb,
                    m->d_hq,     m->d_att,    m->d_logits,   m->d_kt,   m->d_v,    m->d_tokpos, m->d_record,
                    m->d_pf_tok, m->d_pf_x,   m->d_pf_xb,    m->d_pf_q, m->d_pf_hb, m->d_pf_att, m->d_pf_logits,
-                   m->d_pf_xd,  m->d_pf_xc};
+                   m->d_pf_xd,  m->d_pf_xc,  m->d_pf_xc2, m->d_pf_xd2};
     for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_tokpos) hipHostFree(m->h_tokpos);
@@ -738,6 +740,8 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         HIPCHK(hipMalloc((void **)&m->d_pf_logits, sizeof(float) * PP * V));
         HIPCHK(hipMalloc((void **)&m->d_pf_xc, 32 * nbmax * PP));
         HIPCHK(hipMalloc((void **)&m->d_pf_xd, sizeof(float) * nbmax * PP));
+        HIPCHK(hipMalloc((void **)&m->d_pf_xc2, 32 * nbmax * PP));
+        HIPCHK(hipMalloc((void **)&m->d_pf_xd2, sizeof(float) * nbmax * PP));
         HIPCHK(hipMemsetAsync(m->d_pf_xc, 0, 32 * nbmax * PP, g_stream));
         HIPCHK(hipMemsetAsync(m->d_pf_xd, 0, sizeof(float) * nbmax * PP, g_stream));
     }
@@ -947,10 +951,21 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     a.epi = QMH_PF_SWIGLU;
     a.out0 = m->d_pf_hb;
     a.ld0 = H;
+    /* past 32 tokens (the tiled matmul) hb is written only as W2's quantized image */
+    const int hb_image = P > 32;
+    if (hb_image) {
+        a.qxc = m->d_pf_xc2;
+        a.qxd = m->d_pf_xd2;
+        a.qperm8 = L->w2.dtype == QMH_Q4_0;
+    }
     LCHK(qmh_launch_pf_gemm(&a, s));
     /* x += W2 hb */
     pf_args_for(m, &L->w2, P, &a);
-    a.xf = m->d_pf_hb;
+    a.xf = hb_image ? NULL : m->d_pf_hb;
+    if (hb_image) {
+        a.xc = m->d_pf_xc2;
+        a.xd = m->d_pf_xd2;
+    }
     a.ldxf = H;
     a.nxf = H;
     a.norm_w = NULL;
