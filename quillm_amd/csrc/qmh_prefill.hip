@@ -164,16 +164,106 @@ __global__ __launch_bounds__(NT) void k_pf_quant(const float *__restrict__ x, in
     }
 }
 
+// k_pf_quant for rows of n % 4 == 0 values (16-byte aligned rows and gain) in RR rounds: each
+// thread's 4 values of a round are one 16-byte buffer load whose range check (n*4 bytes) zeroes
+// what lies past the row, so all of a thread's loads (row and gain) issue at once, before the
+// sum. The scale 1/sqrt(ss/n + eps) takes the margin test first, as the decode prologue.
+typedef uint32_t pf_v4u __attribute__((ext_vector_type(4)));
+template <int NT, int RR, bool NORM>
+__global__ __launch_bounds__(NT) void k_pf_quant4(const float *__restrict__ x, int ldx, const float *w, float eps,
+                                                      int n, int8_t *xc, float *xd, int PP, int perm8) {
+    __shared__ double red[NT / 64 + 1];
+    const int p = blockIdx.x, tid = threadIdx.x, nb = (n + 31) / 32, sub = tid & 7;
+    const float *row = x + (size_t)p * ldx;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, n * 4, 0x00020000);
+    pf_v4u xv[RR], wv[RR];
+#pragma unroll
+    for (int r = 0; r < RR; r++) xv[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, (r * NT + tid) * 16, 0, 0);
+    float inv = 1.0f;
+    if (NORM) {
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)w, (short)0, n * 4, 0x00020000);
+#pragma unroll
+        for (int r = 0; r < RR; r++) wv[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, (r * NT + tid) * 16, 0, 0);
+        double ss = 0.0;  // values past the row load as +0
+#pragma unroll
+        for (int r = 0; r < RR; r++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const double v = (double)__uint_as_float(xv[r][j]);
+                ss += v * v;
+            }
+        // wave butterflies, then the waves in order; red is not reused, so one barrier publishes
+        ss = qmh_wave_sum_d(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < NT / 64; k++) ss += red[k];
+        // the same ss in every thread: uniform branches
+        if (!qmh_rms_inv_margin(ss, n, nb * 32, eps, &inv)) {
+            const double d = qmh_sum_slack(ss, nb * 32);
+            inv = qmh_rms_inv(ss - d, n, eps);
+            if (inv != qmh_rms_inv(ss + d, n, eps)) {  // the reference's serial sum
+                if (tid == 0) {
+                    double s2 = 0.0;
+                    for (int i = 0; i < n; i++) s2 += (double)row[i] * (double)row[i];
+                    red[NT / 64] = s2;
+                }
+                __syncthreads();
+                inv = qmh_rms_inv(red[NT / 64], n, eps);
+            }
+        }
+    }
+    // (x*inv)*w as the reference; rounds are uniform (DPP needs all 8 lanes of a block)
+#pragma unroll
+    for (int r = 0; r < RR; r++)
+        if (r * (NT / 8) < nb) {
+            const int b = r * (NT / 8) + (tid >> 3), i4 = b * 32 + sub * 4;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float xe = __uint_as_float(xv[r][j]);
+                v[j] = NORM ? ((b < nb && i4 + j < n) ? xe * inv * __uint_as_float(wv[r][j]) : 0.0f) : xe;
+            }
+            pf_quant_block(v, b, nb, p, sub, xc, xd, PP, perm8);
+        }
+}
+
+template <int NT, bool NORM>
+static void pf_quant4_launch(int RR, int P, hipStream_t s, const float *x, int ldx, const float *w, float eps, int n,
+                             int8_t *xc, float *xd, int PP, int perm8) {
+#define PQ4(R_) hipLaunchKernelGGL((k_pf_quant4<NT, R_, NORM>), dim3(P), dim3(NT), 0, s, x, ldx, w, eps, n, xc, xd, PP, perm8)
+    switch (RR) {
+    case 1: PQ4(1); break;
+    case 2: PQ4(2); break;
+    case 4: PQ4(4); break;
+    case 8: PQ4(8); break;
+    default: PQ4(16); break;
+    }
+#undef PQ4
+}
+
 extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc,
                                    float *xd, int PP, int perm8, void *stream) {
     // a few rows (batched decode): 1024 threads per row, one round of loads for a 4096-value row
     // and 16 waves to wait on them; many rows (prefill): 256 threads, more workgroups
-    if (P <= 16)
-        hipLaunchKernelGGL(k_pf_quant<1024>, dim3(P), dim3(1024), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd, PP,
-                           perm8);
-    else
-        hipLaunchKernelGGL(k_pf_quant<QMH_WG>, dim3(P), dim3(QMH_WG), 0, (hipStream_t)stream, x, ldx, w, eps, n, xc, xd,
-                           PP, perm8);
+    const int NT = P <= 16 ? 1024 : QMH_WG, nb = (n + 31) / 32, R = (nb + NT / 8 - 1) / (NT / 8);
+    const bool vec = n % 4 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
+    hipStream_t s = (hipStream_t)stream;
+    if (vec && R <= PQ_R) {
+        const int RR = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : R <= 8 ? 8 : 16;
+        if (NT == 1024) {
+            if (w) pf_quant4_launch<1024, true>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+            else pf_quant4_launch<1024, false>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+        } else {
+            if (w) pf_quant4_launch<QMH_WG, true>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+            else pf_quant4_launch<QMH_WG, false>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+        }
+    } else if (NT == 1024) {
+        hipLaunchKernelGGL(k_pf_quant<1024>, dim3(P), dim3(1024), 0, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+    } else {
+        hipLaunchKernelGGL(k_pf_quant<QMH_WG>, dim3(P), dim3(QMH_WG), 0, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+    }
     return (int)hipGetLastError();
 }
 
