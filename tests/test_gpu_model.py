@@ -155,6 +155,50 @@ def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
         assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
+    """W2's input rows of 202 values (n % 4 == 2): the activation quantizer's per-value path
+    instead of its 16-byte loads (the skinny matmul at 20 tokens), beside the multi-token matvec's
+    own quantization (3 tokens) and W1|W3's image epilogue (40), against sequential forwards.
+    (The batched prefill needs head_dim % 4 == 0, so dim % 4 == 0.)"""
+    import os
+
+    path = str(tmp_path / f"pf_odd_{wt}.qlm")
+    cfg = gpu.QmhConfig(dim=96, hidden_dim=202, n_layers=2, n_heads=8, n_kv_heads=4, vocab_size=300, max_seq=128,
+                        rope_theta=10000.0, norm_eps=1e-5)
+    gpu.gen_model(path, cfg, wt, seed=33, threads=4)
+    chunks = [gpu.prompt_ids(n, 300, seed=20 + n) for n in (40, 20, 3)]
+    runs = []
+    for seq in (False, True):
+        if seq:
+            os.environ["QMH_PREFILL_SEQ"] = "1"
+        try:
+            with gpu.Model.load(path) as m:
+                say(f"case odd {wt}: prefill {'sequential' if seq else 'batched'}")
+                pos, outs = 0, []
+                for ch in chunks:
+                    outs.append(m.prefill(ch, pos, want_logits=True))
+                    pos += len(ch)
+                outs.append(m.forward(5, pos).copy())
+                runs.append(outs)
+        finally:
+            os.environ.pop("QMH_PREFILL_SEQ", None)
+    for got, want in zip(runs[0], runs[1]):
+        assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
+    # batched decode of 6 sequences (the skinny matmul after the quantizer at 1024 threads per row)
+    seqs = [gpu.prompt_ids(4, 300, seed=50 + i) for i in range(6)]
+    with gpu.Model.load(path) as m:
+        say(f"case odd {wt}: batched decode")
+        single = []
+        for s in seqs:
+            single.append(np.stack([m.forward(int(t), k).copy() for k, t in enumerate(s)]))
+        with gpu.Batch(m, 6) as bt:
+            for k in range(4):
+                lg = bt.forward([int(s[k]) for s in seqs], [k] * 6)
+                for i in range(6):
+                    assert np.array_equal(bits(lg[i]), bits(single[i][k])), f"step {k} sequence {i}"
+
+
 @pytest.mark.parametrize("name,dims,wt,spans", [
     # one query head per kv head, head_dim 128: decode attention past one 640-position chunk
     # (positions 638-642 cross into the second chunk, 1279-1281 into the third)
