@@ -1001,6 +1001,85 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_scores(const float *__restrict__ 
         if (k < np && t <= pos0 + p0 + k) att[((size_t)h * P + p0 + k) * max_seq + t] = s[k] * scale;
 }
 
+// The same scores blocked in registers: a workgroup takes 64 tokens x 64 positions, each thread
+// 4 tokens x 4 positions (16 chains). The query and K^T tiles ([HD][64] each) are staged in LDS;
+// per dimension a thread reads 4 query and 4 key values (two 16-byte LDS reads) for 32 VALU
+// operations. (One token x 16 positions per lane needs 16 LDS values per 32 operations, which
+// saturates the LDS return path before the VALU.) Same chains: s = +0, s = s + q[d] * k[d] over d
+// in order, then s * scale.
+template <int HD>
+__global__ __launch_bounds__(QMH_WG) void k_pf_scores_rb(const float *__restrict__ Q, const float *__restrict__ Kt,
+                                                         float *att, int P, int pos0, int n_heads, int n_kv,
+                                                         int max_seq, float scale) {
+    __shared__ __align__(16) float qs[HD * 64];  // [d][token]
+    __shared__ __align__(16) float ks[HD * 64];  // [d][position]
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int p0 = blockIdx.y * 64, c0 = blockIdx.z * 64;
+    if (c0 > pos0 + min(p0 + 63, P - 1)) return;  // the whole tile is past every token (uniform)
+    const int kvh = h / (n_heads / n_kv);
+    const float *kt = Kt + (size_t)kvh * HD * max_seq;
+#pragma unroll
+    for (int k = 0; k < HD * 64 / QMH_WG; k++) {  // K^T rows, coalesced; positions past max_seq read the last
+        const int e = k * QMH_WG + tid, t = c0 + (e & 63);
+        ks[e] = kt[(size_t)(e >> 6) * max_seq + (t < max_seq ? t : max_seq - 1)];
+    }
+    const float *qh = Q + (size_t)h * HD;
+#pragma unroll
+    for (int k = 0; k < HD * 64 / 4 / QMH_WG; k++) {  // 4 dimensions of one token per thread; tokens past P read the last
+        const int e = k * QMH_WG + tid, tok = e & 63, d4 = e >> 6;
+        const int p = p0 + tok < P ? p0 + tok : P - 1;
+        const float4 v = *(const float4 *)(qh + (size_t)p * n_heads * HD + 4 * d4);
+        qs[(4 * d4) * 64 + tok] = v.x;
+        qs[(4 * d4 + 1) * 64 + tok] = v.y;
+        qs[(4 * d4 + 2) * 64 + tok] = v.z;
+        qs[(4 * d4 + 3) * 64 + tok] = v.w;
+    }
+    __syncthreads();
+    const int tg = tid >> 4, pg = tid & 15;  // tokens 4*tg .. +3, positions 4*pg .. +3
+    float s[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) s[a][b] = 0.0f;
+    // dimension d + KA's values are read while dimension d is used. An empty asm per step pins the
+    // chains and the reads to their step: otherwise the compiler hoists every read to the top and
+    // sinks the arithmetic (HD*8 live registers)
+    constexpr int KA = 2;
+    float4 qv[KA + 1], kv[KA + 1];
+#pragma unroll
+    for (int d = 0; d < KA; d++) {
+        qv[d] = *(const float4 *)(qs + d * 64 + 4 * tg);
+        kv[d] = *(const float4 *)(ks + d * 64 + 4 * pg);
+    }
+#pragma unroll
+    for (int d = 0; d < HD; d++) {
+        if (d + KA < HD) {
+            qv[(d + KA) % (KA + 1)] = *(const float4 *)(qs + (d + KA) * 64 + 4 * tg);
+            kv[(d + KA) % (KA + 1)] = *(const float4 *)(ks + (d + KA) * 64 + 4 * pg);
+        }
+        const float4 a4 = qv[d % (KA + 1)], b4 = kv[d % (KA + 1)];
+        const float qa[4] = {a4.x, a4.y, a4.z, a4.w}, kb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) s[a][b] = s[a][b] + qa[a] * kb[b];
+        asm volatile("" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[0][2]), "+v"(s[0][3]), "+v"(s[1][0]), "+v"(s[1][1]),
+                     "+v"(s[1][2]), "+v"(s[1][3]), "+v"(s[2][0]), "+v"(s[2][1]), "+v"(s[2][2]), "+v"(s[2][3]),
+                     "+v"(s[3][0]), "+v"(s[3][1]), "+v"(s[3][2]), "+v"(s[3][3])::"memory");
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int p = p0 + 4 * tg + a;
+        if (p >= P) continue;
+        float *row = att + ((size_t)h * P + p) * max_seq;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int t = c0 + 4 * pg + b;
+            if (t <= pos0 + p) row[t] = s[a][b] * scale;
+        }
+    }
+}
+
 // softmax of one (head, token) row in place (src/ops.c:100-112), one wave per row (4 rows per
 // workgroup): the max and the double sum of the exponentials by shuffles, no barrier. The final
 // pass recomputes each exponential instead of storing and re-reading it (the same bits), so the
@@ -1139,8 +1218,16 @@ extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const fl
     if (hd > 128 || hd % 4 || pos0 + P > max_seq || P < 1) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const int ng = (P + QMH_PF_TOK - 1) / QMH_PF_TOK, nz = (pos0 + P + QMH_WG - 1) / QMH_WG;
-    hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
-                       hd, max_seq, scale);
+    const dim3 gt(n_heads, (P + 63) / 64, (pos0 + P + 63) / 64);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_pf_scores_rb<128>, gt, dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv, max_seq,
+                           scale);
+    else if (hd == 64)
+        hipLaunchKernelGGL(k_pf_scores_rb<64>, gt, dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv, max_seq,
+                           scale);
+    else
+        hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
+                           hd, max_seq, scale);
     hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, (P + QMH_WG / 64 - 1) / (QMH_WG / 64)), dim3(QMH_WG), 0, s, att, P, pos0,
                        max_seq);
     hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd, max_seq);

@@ -155,6 +155,35 @@ def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
         assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("hd,n_heads,n_kv,wt", [(128, 2, 1, "q4_0"), (64, 4, 4, "q8_0"), (64, 4, 2, "q4_0")])
+def test_batched_prefill_head_dims(gpu, tmp_path, hd, n_heads, n_kv, wt):
+    """head_dim 128 and 64 (the register-blocked prefill scores: 64 tokens x 64 positions per
+    workgroup), MHA and GQA, max_seq 301 (not a multiple of 4 or 64: the last tile's positions past
+    max_seq), prompts of 150 then 77 tokens (ragged tiles, pos0 > 0), against sequential forwards."""
+    import os
+
+    path = str(tmp_path / f"pf_hd{hd}_{n_kv}_{wt}.qlm")
+    cfg = gpu.QmhConfig(dim=hd * n_heads, hidden_dim=192, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv,
+                        vocab_size=300, max_seq=301, rope_theta=10000.0, norm_eps=1e-5)
+    gpu.gen_model(path, cfg, wt, seed=35, threads=4)
+    a_ids, b_ids = gpu.prompt_ids(150, 300, seed=61), gpu.prompt_ids(77, 300, seed=62)
+    runs = []
+    for seq in (False, True):
+        if seq:
+            os.environ["QMH_PREFILL_SEQ"] = "1"
+        try:
+            with gpu.Model.load(path) as m:
+                say(f"case hd{hd} kv{n_kv} {wt}: prefill {'sequential' if seq else 'batched'}")
+                a = m.prefill(a_ids, 0, want_logits=True)
+                b = m.prefill(b_ids, 150, want_logits=True)
+                c = m.forward(9, 227).copy()
+                runs.append((a, b, c))
+        finally:
+            os.environ.pop("QMH_PREFILL_SEQ", None)
+    for got, want in zip(runs[0], runs[1]):
+        assert np.array_equal(bits(got), bits(want)), np.abs(got - want).max()
+
+
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
     """W2's input rows of 202 values (n % 4 == 2): the activation quantizer's per-value path
