@@ -1212,6 +1212,105 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att,
         }
 }
 
+// The same P·V blocked in registers for head_dim 128 and 64: each thread extends 4 tokens x 2
+// columns (8 chains), a workgroup 2048/HD tokens. Per position a thread reads the 4 tokens'
+// probabilities (one 16-byte LDS read) and 2 V values (8 bytes) for 16 VALU operations, against 36
+// bytes for the same 16 with one column x 8 tokens per thread, which fills the LDS return path.
+// The chunks, the unmasked runs and the diagonal's selects are as in k_pf_pv.
+template <int HD>
+__global__ __launch_bounds__(QMH_WG) void k_pf_pv_rb(const float *__restrict__ att, const float *__restrict__ V,
+                                                     float *out, int P, int pos0, int n_heads, int n_kv, int max_seq) {
+    constexpr int T = 2048 / HD, VC = QMH_PF_VC;     // tokens per workgroup, positions per chunk
+    constexpr int VR = VC * HD / 4 / QMH_WG;          // float4 of V per thread per chunk
+    constexpr int PR = T * VC / QMH_WG;               // probabilities per thread per chunk
+    __shared__ __align__(16) float ps[VC * T];        // [t][token]
+    __shared__ __align__(16) float vs[VC * HD];       // [t][column]
+    const int h = blockIdx.x, p0 = blockIdx.y * T, np = min(T, P - p0);
+    const int kvh = h / (n_heads / n_kv), kvd = HD * n_kv, tid = threadIdx.x;
+    const int tmax = pos0 + p0 + np;  // positions 0 .. tmax-1 are used by some token
+    const int tall = pos0 + p0 + 1;   // positions 0 .. tall-1 are used by every token of the group
+    const float *vbase = V + (size_t)kvh * HD;
+    pf_v4f vr[VR];  // a vector type: float4 copies became memcpys through a stack slot
+    float pr[PR];
+#define PV_RB_LOAD(C0)                                                                                       \
+    _Pragma("unroll") for (int k = 0; k < VR; k++) {                                        \
+        const int e = k * QMH_WG + tid, t = e / (HD / 4), c4 = e % (HD / 4);                                 \
+        const int tc = (C0) + t < tmax ? (C0) + t : tmax - 1;                                                \
+        vr[k] = *(const pf_v4f *)(vbase + (size_t)tc * kvd + 4 * c4);                                        \
+    }                                                                                                        \
+    _Pragma("unroll") for (int k = 0; k < PR; k++) {                                        \
+        const int e = k * QMH_WG + tid, kk = e / VC, t = (C0) + e % VC;                                      \
+        pr[k] = (kk < np && t <= pos0 + p0 + kk) ? att[((size_t)h * P + p0 + kk) * max_seq + t] : 0.0f;      \
+    }
+    const int tg = tid / (HD / 2), cg = tid % (HD / 2);  // tokens 4*tg .. +3, columns 2*cg, 2*cg + 1
+    float acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; a++) acc[a][0] = acc[a][1] = 0.0f;
+    PV_RB_LOAD(0)
+    for (int c0 = 0; c0 < tmax; c0 += VC) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = k * QMH_WG + tid;
+            *(pf_v4f *)(vs + (e / (HD / 4)) * HD + 4 * (e % (HD / 4))) = vr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < PR; k++) {
+            const int e = k * QMH_WG + tid;
+            ps[(e % VC) * T + e / VC] = pr[k];
+        }
+        if (c0 + VC < tmax) {
+            PV_RB_LOAD(c0 + VC)
+        }
+        __syncthreads();
+        const int nt = min(VC, tmax - c0);
+        const int nall = min(nt, max(tall - c0, 0));  // positions of this chunk every token sees
+        const float *pp = ps + 4 * tg, *vp = vs + 2 * cg;
+        int t = 0;
+        for (; t + 4 <= nall; t += 4) {
+            float4 pa[4];
+            float2 vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                pa[u] = *(const float4 *)(pp + (t + u) * T);
+                vv[u] = *(const float2 *)(vp + (t + u) * HD);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float pk[4] = {pa[u].x, pa[u].y, pa[u].z, pa[u].w};
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    acc[a][0] = acc[a][0] + pk[a] * vv[u].x;
+                    acc[a][1] = acc[a][1] + pk[a] * vv[u].y;
+                }
+            }
+        }
+        for (; t < nt; t++) {
+            const float4 p4 = *(const float4 *)(pp + t * T);
+            const float2 v2 = *(const float2 *)(vp + t * HD);
+            const float pk[4] = {p4.x, p4.y, p4.z, p4.w};
+            const int kmin = c0 + t - (pos0 + p0);  // tokens kk >= kmin see position c0 + t
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const bool on = 4 * tg + a >= kmin;
+                const float n0 = acc[a][0] + pk[a] * v2.x, n1 = acc[a][1] + pk[a] * v2.y;
+                acc[a][0] = on ? n0 : acc[a][0];
+                acc[a][1] = on ? n1 : acc[a][1];
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int kk = 4 * tg + a;
+        if (kk < np) {
+            float *o = out + (size_t)(p0 + kk) * n_heads * HD + h * HD + 2 * cg;
+            o[0] = acc[a][0];
+            o[1] = acc[a][1];
+        }
+    }
+#undef PV_RB_LOAD
+}
+
 extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P,
                                        int pos0, int n_heads, int n_kv, int hd, int max_seq, float scale,
                                        void *stream) {
@@ -1230,6 +1329,14 @@ extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const fl
                            hd, max_seq, scale);
     hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, (P + QMH_WG / 64 - 1) / (QMH_WG / 64)), dim3(QMH_WG), 0, s, att, P, pos0,
                        max_seq);
-    hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd, max_seq);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_pf_pv_rb<128>, dim3(n_heads, (P + 15) / 16), dim3(QMH_WG), 0, s, att, V, out, P, pos0,
+                           n_heads, n_kv, max_seq);
+    else if (hd == 64)
+        hipLaunchKernelGGL(k_pf_pv_rb<64>, dim3(n_heads, (P + 31) / 32), dim3(QMH_WG), 0, s, att, V, out, P, pos0,
+                           n_heads, n_kv, max_seq);
+    else
+        hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd,
+                           max_seq);
     return (int)hipGetLastError();
 }
