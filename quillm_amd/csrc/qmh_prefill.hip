@@ -1011,61 +1011,68 @@ template <int HD>
 __global__ __launch_bounds__(QMH_WG) void k_pf_scores_rb(const float *__restrict__ Q, const float *__restrict__ Kt,
                                                          float *att, int P, int pos0, int n_heads, int n_kv,
                                                          int max_seq, float scale) {
-    __shared__ __align__(16) float qs[HD * 64];  // [d][token]
-    __shared__ __align__(16) float ks[HD * 64];  // [d][position]
+    // the dimensions pass in phases of DP: 32 KB of LDS per workgroup, so that five share a CU and
+    // the causal half of the tiles (1152 of 2048 at 512 tokens) runs in one round
+    constexpr int DP = HD < 64 ? HD : 64;
+    __shared__ __align__(16) float qs[DP * 64];  // [d][token]
+    __shared__ __align__(16) float ks[DP * 64];  // [d][position]
     const int h = blockIdx.x, tid = threadIdx.x;
     const int p0 = blockIdx.y * 64, c0 = blockIdx.z * 64;
     if (c0 > pos0 + min(p0 + 63, P - 1)) return;  // the whole tile is past every token (uniform)
     const int kvh = h / (n_heads / n_kv);
-    const float *kt = Kt + (size_t)kvh * HD * max_seq;
-#pragma unroll
-    for (int k = 0; k < HD * 64 / QMH_WG; k++) {  // K^T rows, coalesced; positions past max_seq read the last
-        const int e = k * QMH_WG + tid, t = c0 + (e & 63);
-        ks[e] = kt[(size_t)(e >> 6) * max_seq + (t < max_seq ? t : max_seq - 1)];
-    }
-    const float *qh = Q + (size_t)h * HD;
-#pragma unroll
-    for (int k = 0; k < HD * 64 / 4 / QMH_WG; k++) {  // 4 dimensions of one token per thread; tokens past P read the last
-        const int e = k * QMH_WG + tid, tok = e & 63, d4 = e >> 6;
-        const int p = p0 + tok < P ? p0 + tok : P - 1;
-        const float4 v = *(const float4 *)(qh + (size_t)p * n_heads * HD + 4 * d4);
-        qs[(4 * d4) * 64 + tok] = v.x;
-        qs[(4 * d4 + 1) * 64 + tok] = v.y;
-        qs[(4 * d4 + 2) * 64 + tok] = v.z;
-        qs[(4 * d4 + 3) * 64 + tok] = v.w;
-    }
-    __syncthreads();
     const int tg = tid >> 4, pg = tid & 15;  // tokens 4*tg .. +3, positions 4*pg .. +3
     float s[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) s[a][b] = 0.0f;
-    // dimension d + KA's values are read while dimension d is used. An empty asm per step pins the
-    // chains and the reads to their step: otherwise the compiler hoists every read to the top and
-    // sinks the arithmetic (HD*8 live registers)
-    constexpr int KA = 2;
-    float4 qv[KA + 1], kv[KA + 1];
 #pragma unroll
-    for (int d = 0; d < KA; d++) {
-        qv[d] = *(const float4 *)(qs + d * 64 + 4 * tg);
-        kv[d] = *(const float4 *)(ks + d * 64 + 4 * pg);
-    }
+    for (int d0 = 0; d0 < HD; d0 += DP) {
+        if (d0) __syncthreads();  // the previous phase's reads are done
+        const float *kt = Kt + ((size_t)kvh * HD + d0) * max_seq;
 #pragma unroll
-    for (int d = 0; d < HD; d++) {
-        if (d + KA < HD) {
-            qv[(d + KA) % (KA + 1)] = *(const float4 *)(qs + (d + KA) * 64 + 4 * tg);
-            kv[(d + KA) % (KA + 1)] = *(const float4 *)(ks + (d + KA) * 64 + 4 * pg);
+        for (int k = 0; k < DP * 64 / QMH_WG; k++) {  // K^T rows, coalesced; positions past max_seq read the last
+            const int e = k * QMH_WG + tid, t = c0 + (e & 63);
+            ks[e] = kt[(size_t)(e >> 6) * max_seq + (t < max_seq ? t : max_seq - 1)];
         }
-        const float4 a4 = qv[d % (KA + 1)], b4 = kv[d % (KA + 1)];
-        const float qa[4] = {a4.x, a4.y, a4.z, a4.w}, kb[4] = {b4.x, b4.y, b4.z, b4.w};
+        const float *qh = Q + (size_t)h * HD + d0;
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int k = 0; k < DP * 64 / 4 / QMH_WG; k++) {  // 4 dimensions of one token per thread; tokens past P read the last
+            const int e = k * QMH_WG + tid, tok = e & 63, d4 = e >> 6;
+            const int p = p0 + tok < P ? p0 + tok : P - 1;
+            const float4 v = *(const float4 *)(qh + (size_t)p * n_heads * HD + 4 * d4);
+            qs[(4 * d4) * 64 + tok] = v.x;
+            qs[(4 * d4 + 1) * 64 + tok] = v.y;
+            qs[(4 * d4 + 2) * 64 + tok] = v.z;
+            qs[(4 * d4 + 3) * 64 + tok] = v.w;
+        }
+        __syncthreads();
+        // dimension d + KA's values are read while dimension d is used. An empty asm per step pins
+        // the chains and the reads to their step: otherwise the compiler hoists every read to the
+        // top and sinks the arithmetic (DP*8 live registers)
+        constexpr int KA = 2;
+        float4 qv[KA + 1], kv[KA + 1];
 #pragma unroll
-            for (int b = 0; b < 4; b++) s[a][b] = s[a][b] + qa[a] * kb[b];
-        asm volatile("" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[0][2]), "+v"(s[0][3]), "+v"(s[1][0]), "+v"(s[1][1]),
-                     "+v"(s[1][2]), "+v"(s[1][3]), "+v"(s[2][0]), "+v"(s[2][1]), "+v"(s[2][2]), "+v"(s[2][3]),
-                     "+v"(s[3][0]), "+v"(s[3][1]), "+v"(s[3][2]), "+v"(s[3][3])::"memory");
+        for (int d = 0; d < KA; d++) {
+            qv[d] = *(const float4 *)(qs + d * 64 + 4 * tg);
+            kv[d] = *(const float4 *)(ks + d * 64 + 4 * pg);
+        }
+#pragma unroll
+        for (int d = 0; d < DP; d++) {
+            if (d + KA < DP) {
+                qv[(d + KA) % (KA + 1)] = *(const float4 *)(qs + (d + KA) * 64 + 4 * tg);
+                kv[(d + KA) % (KA + 1)] = *(const float4 *)(ks + (d + KA) * 64 + 4 * pg);
+            }
+            const float4 a4 = qv[d % (KA + 1)], b4 = kv[d % (KA + 1)];
+            const float qa[4] = {a4.x, a4.y, a4.z, a4.w}, kb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) s[a][b] = s[a][b] + qa[a] * kb[b];
+            asm volatile("" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[0][2]), "+v"(s[0][3]), "+v"(s[1][0]), "+v"(s[1][1]),
+                         "+v"(s[1][2]), "+v"(s[1][3]), "+v"(s[2][0]), "+v"(s[2][1]), "+v"(s[2][2]), "+v"(s[2][3]),
+                         "+v"(s[3][0]), "+v"(s[3][1]), "+v"(s[3][2]), "+v"(s[3][3])::"memory");
+        }
     }
 #pragma unroll
     for (int a = 0; a < 4; a++) {
@@ -1225,7 +1232,12 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv_rb(const float *__restrict__ a
     constexpr int PR = T * VC / QMH_WG;               // probabilities per thread per chunk
     __shared__ __align__(16) float ps[VC * T];        // [t][token]
     __shared__ __align__(16) float vs[VC * HD];       // [t][column]
-    const int h = blockIdx.x, p0 = blockIdx.y * T, np = min(T, P - p0);
+    // token groups by quadrant of blockIdx.y, the odd quadrants reversed: the workgroups that share
+    // a CU (y = g, g + ng/4, g + ng/2, g + 3ng/4 when all are resident at once) then carry equal
+    // work in sum (late groups see more positions)
+    const int ng = gridDim.y, q4 = ng / 4, gy = blockIdx.y;
+    const int grp = (ng % 4 == 0 && (gy / q4) % 2 == 1) ? (gy / q4) * q4 + (q4 - 1 - gy % q4) : gy;
+    const int h = blockIdx.x, p0 = grp * T, np = min(T, P - p0);
     const int kvh = h / (n_heads / n_kv), kvd = HD * n_kv, tid = threadIdx.x;
     const int tmax = pos0 + p0 + np;  // positions 0 .. tmax-1 are used by some token
     const int tall = pos0 + p0 + 1;   // positions 0 .. tall-1 are used by every token of the group
@@ -1233,12 +1245,12 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv_rb(const float *__restrict__ a
     pf_v4f vr[VR];  // a vector type: float4 copies became memcpys through a stack slot
     float pr[PR];
 #define PV_RB_LOAD(C0)                                                                                       \
-    _Pragma("unroll") for (int k = 0; k < VR; k++) {                                        \
+    _Pragma("unroll") for (int k = 0; k < VR; k++) {                                                         \
         const int e = k * QMH_WG + tid, t = e / (HD / 4), c4 = e % (HD / 4);                                 \
         const int tc = (C0) + t < tmax ? (C0) + t : tmax - 1;                                                \
         vr[k] = *(const pf_v4f *)(vbase + (size_t)tc * kvd + 4 * c4);                                        \
     }                                                                                                        \
-    _Pragma("unroll") for (int k = 0; k < PR; k++) {                                        \
+    _Pragma("unroll") for (int k = 0; k < PR; k++) {                                                         \
         const int e = k * QMH_WG + tid, kk = e / VC, t = (C0) + e % VC;                                      \
         pr[k] = (kk < np && t <= pos0 + p0 + kk) ? att[((size_t)h * P + p0 + kk) * max_seq + t] : 0.0f;      \
     }
