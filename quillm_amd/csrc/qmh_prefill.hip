@@ -1115,6 +1115,49 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_softmax(float *att, int P, int po
     for (int t = lane; t < n; t += 64) x[t] = qmh_expf(x[t] - m) * inv;
 }
 
+// k_pf_softmax with the row in registers (rows of up to 64*R positions): one range-checked load
+// per value, all issued at once; each exponential is computed once and kept for both the sum and
+// the probability (the same values k_pf_softmax computes twice). The serial fallback reads the
+// scores, which stay untouched until the final stores.
+template <int R>
+__global__ __launch_bounds__(QMH_WG) void k_pf_softmax_r(float *att, int P, int pos0, int max_seq) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: a scalar resource
+    const int h = blockIdx.x, p = blockIdx.y * (QMH_WG / 64) + wave, lane = threadIdx.x & 63;
+    if (p >= P) return;  // the whole wave
+    const int n = pos0 + p + 1;
+    float *x = att + ((size_t)h * P + p) * max_seq;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, n * 4, 0x00020000);
+    float xv[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) xv[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (r * 64 + lane) * 4, 0, 0));
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (r * 64 + lane < n) m = xv[r] > m ? xv[r] : m;
+    m = qmh_wave_max(m);
+    const float x0 = __shfl(xv[0], 0);
+    if (x0 != x0) m = x0;  // the reference's scan starts from x[0]: a NaN there stays
+    float e[R];
+    double sum = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        e[r] = qmh_expf(xv[r] - m);
+        if (r * 64 + lane < n) sum += (double)e[r];
+    }
+    sum = qmh_wave_sum_d(sum);
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform; serial sum as the reference
+        double ser = 0.0;
+        if (lane == 0)
+            for (int t = 0; t < n; t++) ser += (double)qmh_expf(x[t] - m);
+        inv = qmh_recip_of_sum(__shfl(ser, 0));
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (r * 64 + lane < n) x[r * 64 + lane] = e[r] * inv;
+}
+
 // out[token][h*hd + i] = +0 + p_0 v_0[i] + p_1 v_1[i] + ... in position order (src/model.c:147-154);
 // one workgroup per (head, 16 tokens), head_dim <= 128. V and the probabilities pass through LDS
 // in chunks of 64 positions (cooperative float4 loads, the next chunk's held in registers while
@@ -1339,8 +1382,12 @@ extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const fl
     else
         hipLaunchKernelGGL(k_pf_scores, dim3(n_heads, ng, nz), dim3(QMH_WG), 0, s, Q, Kt, att, P, pos0, n_heads, n_kv,
                            hd, max_seq, scale);
-    hipLaunchKernelGGL(k_pf_softmax, dim3(n_heads, (P + QMH_WG / 64 - 1) / (QMH_WG / 64)), dim3(QMH_WG), 0, s, att, P, pos0,
-                       max_seq);
+    const dim3 gs(n_heads, (P + QMH_WG / 64 - 1) / (QMH_WG / 64));
+    const int rlen = pos0 + P;  // the longest row
+    if (rlen <= 64 * 4) hipLaunchKernelGGL(k_pf_softmax_r<4>, gs, dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
+    else if (rlen <= 64 * 8) hipLaunchKernelGGL(k_pf_softmax_r<8>, gs, dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
+    else if (rlen <= 64 * 16) hipLaunchKernelGGL(k_pf_softmax_r<16>, gs, dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
+    else hipLaunchKernelGGL(k_pf_softmax, gs, dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
     if (hd == 128)
         hipLaunchKernelGGL(k_pf_pv_rb<128>, dim3(n_heads, (P + 15) / 16), dim3(QMH_WG), 0, s, att, V, out, P, pos0,
                            n_heads, n_kv, max_seq);
