@@ -125,9 +125,12 @@ int qmh_launch_pf_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, 
 int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc, float *xd,
                         int PP, int perm8, void *stream);
 int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream);
-/* causal attention of P tokens at positions pos0.. over the caches; att: scratch [n_heads][P][max_seq] */
+/* causal attention of P tokens at positions pos0.. over the caches; att: scratch [n_heads][P][max_seq].
+ * xc != NULL (head_dim 128 or 64 only): out is also written as its Q8_0 image (xc, xd, PP tokens per
+ * block, perm8: the Q4_0 consumers' byte order), as qmh_launch_pf_quant would write it */
 int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P, int pos0,
-                            int n_heads, int n_kv, int hd, int max_seq, float scale, void *stream);
+                            int n_heads, int n_kv, int hd, int max_seq, float scale, int8_t *xc, float *xd, int PP,
+                            int perm8, void *stream);
 
 /* attention of B independent sequences, one query each (src/model.c:127-156 per sequence): sequence b
  * at position pos[b] (device), query Q[b][n_heads*hd], caches Kt + b*kv_stride ([kvd][max_seq]) and

@@ -246,8 +246,9 @@ static void pf_quant4_launch(int RR, int P, hipStream_t s, const float *x, int l
 extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, float eps, int n, int P, int8_t *xc,
                                    float *xd, int PP, int perm8, void *stream) {
     // a few rows (batched decode): 1024 threads per row, one round of loads for a 4096-value row
-    // and 16 waves to wait on them; many rows (prefill): 256 threads, more workgroups
-    const int NT = P <= 16 ? 1024 : QMH_WG, nb = (n + 31) / 32, R = (nb + NT / 8 - 1) / (NT / 8);
+    // and 16 waves to wait on them; many rows (prefill): 512 threads (256 and 1024 were 0.3-0.5%
+    // slower at 512 rows)
+    const int NT = P <= 16 ? 1024 : 512, nb = (n + 31) / 32, R = (nb + NT / 8 - 1) / (NT / 8);
     const bool vec = n % 4 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
     hipStream_t s = (hipStream_t)stream;
     if (vec && R <= PQ_R) {
@@ -256,8 +257,8 @@ extern "C" int qmh_launch_pf_quant(const float *x, int ldx, const float *w, floa
             if (w) pf_quant4_launch<1024, true>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
             else pf_quant4_launch<1024, false>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
         } else {
-            if (w) pf_quant4_launch<QMH_WG, true>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
-            else pf_quant4_launch<QMH_WG, false>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+            if (w) pf_quant4_launch<512, true>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
+            else pf_quant4_launch<512, false>(RR, P, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
         }
     } else if (NT == 1024) {
         hipLaunchKernelGGL(k_pf_quant<1024>, dim3(P), dim3(1024), 0, s, x, ldx, w, eps, n, xc, xd, PP, perm8);
@@ -1269,7 +1270,8 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv(const float *__restrict__ att,
 // The chunks, the unmasked runs and the diagonal's selects are as in k_pf_pv.
 template <int HD>
 __global__ __launch_bounds__(QMH_WG) void k_pf_pv_rb(const float *__restrict__ att, const float *__restrict__ V,
-                                                     float *out, int P, int pos0, int n_heads, int n_kv, int max_seq) {
+                                                     float *out, int P, int pos0, int n_heads, int n_kv, int max_seq,
+                                                     int8_t *xc, float *xd, int PP, int perm8) {
     constexpr int T = 2048 / HD, VC = QMH_PF_VC;     // tokens per workgroup, positions per chunk
     constexpr int VR = VC * HD / 4 / QMH_WG;          // float4 of V per thread per chunk
     constexpr int PR = T * VC / QMH_WG;               // probabilities per thread per chunk
@@ -1363,13 +1365,57 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_pv_rb(const float *__restrict__ a
             o[1] = acc[a][1];
         }
     }
+    if (xc) {  // uniform
+        // Wo's input as its Q8_0 image (the quantizer's steps, src/quant.c:27-52): block b of a token
+        // is columns 32*(cg/16) .. +31 of the head, held by the 16 lanes of cg/16 (values 2j, 2j+1 of
+        // the block in lane j = cg % 16): amax over those lanes, the fp16 scale, the codes. Q4_0
+        // consumers take each 8-group as e0 e2 e4 e6 e1 e3 e5 e7: lane j's two codes are bytes j % 4
+        // and 4 + j % 4 of group j / 4.
+        const int j = cg & 15, b = h * (HD / 32) + (cg >> 4);
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const int kk = 4 * tg + a;
+            float m = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float av = fabsf(acc[a][c]);
+                m = av > m ? av : m;
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const float t = __shfl_xor(m, o);
+                m = t > m ? t : m;
+            }
+            const float dd = qmh_h2f(qmh_f2h(qmh_div127(m)));
+            const float v4[4] = {acc[a][0], acc[a][1], 0.0f, 0.0f};
+            int q[4];
+            qmh_q8_codes4(v4, dd, qmh_rcp(dd), q);
+            const uint32_t c0 = (uint32_t)q[0] & 0xffu, c1 = (uint32_t)q[1] & 0xffu;
+            int8_t *blk = xc + ((size_t)b * PP + p0 + kk) * 32;
+            if (perm8) {
+                uint32_t w0 = c0 << (8 * (j & 3)), w1 = c1 << (8 * (j & 3));
+                w0 |= (uint32_t)__shfl_xor((int)w0, 1);
+                w1 |= (uint32_t)__shfl_xor((int)w1, 1);
+                w0 |= (uint32_t)__shfl_xor((int)w0, 2);
+                w1 |= (uint32_t)__shfl_xor((int)w1, 2);
+                if (kk < np && (j & 3) == 0) *(uint2 *)(blk + 8 * (j >> 2)) = make_uint2(w0, w1);
+            } else {
+                uint32_t w = (c0 | (c1 << 8)) << (16 * (j & 1));
+                w |= (uint32_t)__shfl_xor((int)w, 1);
+                if (kk < np && (j & 1) == 0) *(uint32_t *)(blk + 2 * j) = w;
+            }
+            if (kk < np && j == 0) xd[(size_t)b * PP + p0 + kk] = dd;
+        }
+    }
 #undef PV_RB_LOAD
 }
 
 extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, float *att, float *out, int P,
-                                       int pos0, int n_heads, int n_kv, int hd, int max_seq, float scale,
-                                       void *stream) {
+                                       int pos0, int n_heads, int n_kv, int hd, int max_seq, float scale, int8_t *xc,
+                                       float *xd, int PP, int perm8, void *stream) {
     if (hd > 128 || hd % 4 || pos0 + P > max_seq || P < 1) return (int)hipErrorInvalidValue;
+    // the output's quantized image comes only from the register-blocked P.V (head_dim 128 or 64)
+    if (xc && (!xd || (hd != 128 && hd != 64) || P > PP)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const int ng = (P + QMH_PF_TOK - 1) / QMH_PF_TOK, nz = (pos0 + P + QMH_WG - 1) / QMH_WG;
     const dim3 gt(n_heads, (P + 63) / 64, (pos0 + P + 63) / 64);
@@ -1390,10 +1436,10 @@ extern "C" int qmh_launch_pf_attention(const float *Q, const float *Kt, const fl
     else hipLaunchKernelGGL(k_pf_softmax, gs, dim3(QMH_WG), 0, s, att, P, pos0, max_seq);
     if (hd == 128)
         hipLaunchKernelGGL(k_pf_pv_rb<128>, dim3(n_heads, (P + 15) / 16), dim3(QMH_WG), 0, s, att, V, out, P, pos0,
-                           n_heads, n_kv, max_seq);
+                           n_heads, n_kv, max_seq, xc, xd, PP, perm8);
     else if (hd == 64)
         hipLaunchKernelGGL(k_pf_pv_rb<64>, dim3(n_heads, (P + 31) / 32), dim3(QMH_WG), 0, s, att, V, out, P, pos0,
-                           n_heads, n_kv, max_seq);
+                           n_heads, n_kv, max_seq, xc, xd, PP, perm8);
     else
         hipLaunchKernelGGL(k_pf_pv, dim3(n_heads, ng), dim3(QMH_WG), 0, s, att, V, out, P, pos0, n_heads, n_kv, hd,
                            max_seq);

@@ -924,12 +924,15 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     if (bt)
         LCHK(qmh_launch_bt_attention(m->d_pf_q, kl, vl, bt->kv_stride, bt->pos, bt->max_pos, m->d_pf_att, m->d_pf_xb,
                                      P, c->n_heads, c->n_kv_heads, m->hd, S_, 1.0f / sqrtf((float)m->hd), 0, s));
-    else
+    /* head_dim 128 or 64: P.V also writes xb as Wo's quantized input image */
+    const int xb_image = !bt && (m->hd == 128 || m->hd == 64);
+    if (!bt)
         LCHK(qmh_launch_pf_attention(m->d_pf_q, kl, vl, m->d_pf_att, m->d_pf_xb, P, pos, c->n_heads, c->n_kv_heads,
-                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), s));
+                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), xb_image ? m->d_pf_xc : NULL,
+                                     xb_image ? m->d_pf_xd : NULL, m->pf_pp, L->wo.dtype == QMH_Q4_0, s));
     /* x += Wo xb */
     pf_args_for(m, &L->wo, P, &a);
-    a.xf = m->d_pf_xb;
+    a.xf = xb_image ? NULL : m->d_pf_xb;
     a.ldxf = D;
     a.nxf = D;
     a.norm_w = NULL;

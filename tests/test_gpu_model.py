@@ -157,16 +157,18 @@ def test_batched_prefill_matches_sequential(gpu, tmp_path, wt):
 
 @pytest.mark.parametrize("hd,n_heads,n_kv,wt", [(128, 2, 1, "q4_0"), (64, 4, 4, "q8_0"), (64, 4, 2, "q4_0")])
 def test_batched_prefill_head_dims(gpu, tmp_path, hd, n_heads, n_kv, wt):
-    """head_dim 128 and 64 (the register-blocked prefill scores: 64 tokens x 64 positions per
-    workgroup), MHA and GQA, max_seq 301 (not a multiple of 4 or 64: the last tile's positions past
-    max_seq), prompts of 150 then 77 tokens (ragged tiles, pos0 > 0), against sequential forwards."""
+    """head_dim 128 and 64 (the register-blocked prefill attention: scores of 64 tokens x 64
+    positions per workgroup, P.V writing Wo's quantized input image), MHA and GQA, max_seq 301 (not
+    a multiple of 4 or 64: the last tile's positions past max_seq), prompts of 150, 77, 20 and 3
+    tokens (ragged tiles, pos0 > 0; Wo as the tiled matmul, the skinny matmul and the multi-token
+    matvec, each reading that image), against sequential forwards."""
     import os
 
     path = str(tmp_path / f"pf_hd{hd}_{n_kv}_{wt}.qlm")
     cfg = gpu.QmhConfig(dim=hd * n_heads, hidden_dim=192, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv,
                         vocab_size=300, max_seq=301, rope_theta=10000.0, norm_eps=1e-5)
     gpu.gen_model(path, cfg, wt, seed=35, threads=4)
-    a_ids, b_ids = gpu.prompt_ids(150, 300, seed=61), gpu.prompt_ids(77, 300, seed=62)
+    chunks = [gpu.prompt_ids(n, 300, seed=61 + n) for n in (150, 77, 20, 3)]
     runs = []
     for seq in (False, True):
         if seq:
@@ -174,10 +176,12 @@ def test_batched_prefill_head_dims(gpu, tmp_path, hd, n_heads, n_kv, wt):
         try:
             with gpu.Model.load(path) as m:
                 say(f"case hd{hd} kv{n_kv} {wt}: prefill {'sequential' if seq else 'batched'}")
-                a = m.prefill(a_ids, 0, want_logits=True)
-                b = m.prefill(b_ids, 150, want_logits=True)
-                c = m.forward(9, 227).copy()
-                runs.append((a, b, c))
+                pos, outs = 0, []
+                for ch in chunks:
+                    outs.append(m.prefill(ch, pos, want_logits=True))
+                    pos += len(ch)
+                outs.append(m.forward(9, pos).copy())
+                runs.append(outs)
         finally:
             os.environ.pop("QMH_PREFILL_SEQ", None)
     for got, want in zip(runs[0], runs[1]):
