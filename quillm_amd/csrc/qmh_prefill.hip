@@ -1142,8 +1142,11 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_softmax_r(float *att, int P, int 
     double sum = 0.0;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        e[r] = qmh_expf(xv[r] - m);
-        if (r * 64 + lane < n) sum += (double)e[r];
+        e[r] = 0.0f;
+        if (r * 64 < n) {  // uniform: rounds past the row cost nothing (rows are 1 .. 64*R long)
+            e[r] = qmh_expf(xv[r] - m);
+            if (r * 64 + lane < n) sum += (double)e[r];
+        }
     }
     sum = qmh_wave_sum_d(sum);
     const double d = qmh_sum_slack(sum, n);
