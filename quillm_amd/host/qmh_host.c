@@ -1015,7 +1015,9 @@ static int pf_batched(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
                 HIPCHK(hipMemcpyAsync(host + (mode == PF_LOGITS_ALL ? (size_t)c0 * V : 0), m->d_pf_logits,
                                       sizeof(float) * (size_t)rows * V, hipMemcpyDeviceToHost, g_stream));
         }
-        HIPCHK(hipStreamSynchronize(g_stream)); /* h_pf_tok is reused by the next pass */
+        /* h_pf_tok is reused by the next pass; after the last one the caller synchronizes (the
+           timed prefill records its end event first) */
+        if (c0 + P < n) HIPCHK(hipStreamSynchronize(g_stream));
     }
     return 0;
 }
@@ -1024,8 +1026,11 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
     if (!m || !tokens || n < 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.max_seq) return fail("prefill: bad range");
     for (int32_t i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) return fail("prefill: token %d out of range", tokens[i]);
-    if (m->pf_ok && getenv("QMH_PREFILL_SEQ") == NULL)
-        return pf_batched(m, tokens, n, pos0, logits ? PF_LOGITS_ALL : PF_LOGITS_NONE, logits);
+    if (m->pf_ok && getenv("QMH_PREFILL_SEQ") == NULL) {
+        if (pf_batched(m, tokens, n, pos0, logits ? PF_LOGITS_ALL : PF_LOGITS_NONE, logits)) return -1;
+        HIPCHK(hipStreamSynchronize(g_stream));
+        return 0;
+    }
     const size_t V = (size_t)m->cfg.vocab_size;
     for (int32_t i = 0; i < n; i++) {
         int32_t *slot = m->h_tokpos + 4 * (size_t)i;
