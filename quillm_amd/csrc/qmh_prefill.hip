@@ -35,21 +35,40 @@ __global__ void k_pf_embed(const uint8_t *__restrict__ E, int dtype, int dim, in
     int tok = tokens[p];
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);  // the host validated the ids
     const size_t nbr = (size_t)(dim + 31) / 32;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-        const int b = i >> 5, k = i & 31;
-        float v;
-        if (dtype == QMH_Q8) {
-            const uint8_t *blk = E + ((size_t)tok * nbr + b) * 34;
-            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(int8_t)blk[2 + k];
-        } else if (dtype == QMH_Q4) {
-            const uint8_t *blk = E + ((size_t)tok * nbr + b) * 18;
-            const uint8_t byte = blk[2 + (k >> 1)];
-            const int q = (k & 1) ? (byte >> 4) : (byte & 15);
-            v = qmh_h2f((uint16_t)(blk[0] | (blk[1] << 8))) * (float)(q - 8);
-        } else {
-            v = ((const float *)E)[(size_t)tok * dim + i];
+    float *xr = X + (size_t)p * dim;
+    if (dtype == QMH_Q8 || dtype == QMH_Q4) {
+        // a quarter block (8 values) per thread: the scale, then the codes as 16-bit loads (a block's
+        // codes start 2 bytes in, so they are only 2-byte aligned)
+        const int bs = dtype == QMH_Q8 ? 34 : 18;
+        for (int g = threadIdx.x; g < (int)nbr * 4; g += blockDim.x) {
+            const int b = g >> 2, k0 = (g & 3) * 8;
+            if (b * 32 + k0 >= dim) continue;
+            const uint8_t *blk = E + ((size_t)tok * nbr + b) * bs;
+            const float d = qmh_h2f(*(const uint16_t *)blk);
+            float v[8];
+            if (dtype == QMH_Q8) {
+                const uint16_t *c = (const uint16_t *)(blk + 2 + k0);
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const uint16_t w = c[h];
+                    v[2 * h] = d * (float)(int8_t)(w & 0xff);
+                    v[2 * h + 1] = d * (float)(int8_t)(w >> 8);
+                }
+            } else {
+                const uint16_t *c = (const uint16_t *)(blk + 2 + k0 / 2);  // element k: byte k/2, low nibble first
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint16_t w = c[h];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) v[4 * h + q] = d * (float)((int)((w >> (4 * q)) & 15) - 8);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (b * 32 + k0 + k < dim) xr[b * 32 + k0 + k] = v[k];
         }
-        X[(size_t)p * dim + i] = v;
+    } else {
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) xr[i] = ((const float *)E)[(size_t)tok * dim + i];
     }
 }
 
