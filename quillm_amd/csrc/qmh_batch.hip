@@ -119,12 +119,13 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_pv(const float *__restrict__ att,
 
 // The three steps above in one workgroup per (head blockIdx.x, sequence blockIdx.y), for contexts
 // of at most BT_FUSE_MAX positions: the scores and then the probabilities stay in LDS (P), V
-// passes through LDS BT_FC positions at a time (chunk 0 is loaded before the scores start, chunk
-// c+1 while chunk c is added). The sums are the same chains in the same order.
+// passes through LDS BT_FC positions at a time as the products p_t * v_t (chunk 0 is loaded
+// before the scores start, chunk c+1 while chunk c is added). The sums are the same chains in the
+// same order.
 constexpr int BT_T = 1024;
 constexpr int BT_FC = 128;
 constexpr int BT_FUSE_MAX = 16384;
-__global__ __launch_bounds__(BT_T) void k_bt_attn(const float *__restrict__ Q, const float *__restrict__ Kt,
+__global__ __launch_bounds__(BT_T, 8) void k_bt_attn(const float *__restrict__ Q, const float *__restrict__ Kt,
                                                   const float *__restrict__ V, long long kv_stride,
                                                   const int32_t *__restrict__ pos_arr, float *out, int n_heads,
                                                   int n_kv, int hd, int max_seq, float scale) {
@@ -150,18 +151,19 @@ __global__ __launch_bounds__(BT_T) void k_bt_attn(const float *__restrict__ Q, c
     load(0);
     if (tid < hd) qs[tid] = Q[(size_t)b * n_heads * hd + h * hd + tid];
     __syncthreads();
-    // scores: position t is lane t's chain over head_dim (64 K loads in flight)
+    // scores: position t is lane t's chain over head_dim (32 K loads in flight: with the V registers
+    // the kernel fits 64 VGPRs, so two workgroups share a CU)
     const float *kc = Kt + (size_t)b * kv_stride + (size_t)kvh * hd * max_seq;
     for (int t0 = 0; t0 < n; t0 += BT_T) {
         if (t0 + (tid & ~63) >= n) break;  // whole wave past the context
         const int t = t0 + tid, tc = t < n ? t : n - 1;
         float s = 0.0f;
-        for (int d0 = 0; d0 < hd; d0 += 64) {
-            float kv[64];
+        for (int d0 = 0; d0 < hd; d0 += 32) {
+            float kv[32];
 #pragma unroll
-            for (int j = 0; j < 64; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq + tc];
+            for (int j = 0; j < 32; j++) kv[j] = kc[(size_t)(d0 + j < hd ? d0 + j : hd - 1) * max_seq + tc];
 #pragma unroll
-            for (int j = 0; j < 64; j++)
+            for (int j = 0; j < 32; j++)
                 if (d0 + j < hd) s = s + qs[d0 + j] * kv[j];
         }
         if (t < n) P[t] = s * scale;
@@ -192,21 +194,23 @@ __global__ __launch_bounds__(BT_T) void k_bt_attn(const float *__restrict__ Q, c
         inv = qmh_recip_of_sum(red[BT_T / 64]);
     }
     for (int t = tid; t < n; t += BT_T) P[t] = P[t] * inv;
-    // P·V: lane i < hd runs column i's chain over the staged chunks
+    // P·V: every thread stages the products p_t * v_t of its V float4 (the rounded products the
+    // chain would form), then lane i < hd runs column i's chain of adds over the chunk
     float acc = 0.0f;
     for (int c0 = 0; c0 < n; c0 += BT_FC) {
         __syncthreads();  // P final (first chunk); the previous chunk's reads done
 #pragma unroll
         for (int k = 0; k < VR; k++) {
-            const int e = k * BT_T + tid;
-            *(float4 *)(vs + (e >> 5) * 128 + 4 * (e & 31)) = vr[k];
+            const int e = k * BT_T + tid, t = e >> 5;
+            const float p = P[c0 + t < n ? c0 + t : n - 1];
+            const float4 v = vr[k];
+            *(float4 *)(vs + t * 128 + 4 * (e & 31)) = make_float4(p * v.x, p * v.y, p * v.z, p * v.w);
         }
         if (c0 + BT_FC < n) load(c0 + BT_FC);
         __syncthreads();
         if (tid < hd) {
             const int nt = min(BT_FC, n - c0);
-            const float *pc = P + c0;
-            for (int t = 0; t < nt; t++) acc = acc + pc[t] * vs[t * 128 + tid];
+            for (int t = 0; t < nt; t++) acc = acc + vs[t * 128 + tid];
         }
     }
     if (tid < hd) out[(size_t)b * n_heads * hd + h * hd + tid] = acc;
