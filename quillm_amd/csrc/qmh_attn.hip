@@ -20,12 +20,19 @@
 // HD > 0: head_dim known at compile time -- all HD loads of a lane are issued before its chain
 // starts (maximum bytes in flight); HD == 0: any head_dim, loads in groups of 16. The query
 // is read with uniform (scalar) loads: every lane of the wave needs the same q values.
+// blockIdx.z: the sequence of a batched decode step (its query, caches at Kt + z*kv_stride, score
+// rows and position pos_ptr[z]); 0 for the single sequence.
 template <int HD>
 __global__ __launch_bounds__(QMH_SC_T) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ Kt,
                                                           float *__restrict__ att, const int32_t *pos_ptr,
-                                                          int n_heads, int n_kv, int hd_rt, int max_seq, float scale) {
+                                                          int n_heads, int n_kv, int hd_rt, int max_seq, float scale,
+                                                          long long kv_stride) {
     const int hd = HD > 0 ? HD : hd_rt;
-    const int pos = *pos_ptr;
+    const int z = blockIdx.z;
+    q += (size_t)z * n_heads * hd;
+    Kt += z * kv_stride;
+    att += (size_t)z * n_heads * max_seq;
+    const int pos = pos_ptr[z];
     const int t0 = blockIdx.y * QMH_SC_T;
     if (pos < 0 || pos >= max_seq || t0 > pos) return;
     const int kvh = blockIdx.x, group = n_heads / n_kv;
@@ -71,7 +78,7 @@ extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float
                                            stream);
 #define QMH_SC(HD) \
     hipLaunchKernelGGL(k_attn_scores<HD>, grid, dim3(QMH_SC_T), 0, s, q, kcache, att, pos_ptr, n_heads, n_kv_heads, \
-                       head_dim, max_seq, scale)
+                       head_dim, max_seq, scale, 0LL)
     if (head_dim == 128) QMH_SC(128);
     else if (head_dim == 64) QMH_SC(64);
     else if (head_dim == 48) QMH_SC(48);
@@ -393,7 +400,7 @@ __device__ __forceinline__ void pv_mha_long(const float *__restrict__ s0, const 
 template <int TC>
 __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict__ att, const float *__restrict__ V,
                                                         float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
-                                                        int n_kv, int hd, int max_seq) {
+                                                        int n_kv, int hd, int max_seq, long long kv_stride) {
     constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
     constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
     constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
@@ -407,7 +414,12 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     __shared__ double wsum[QMH_WG / 64];
     __shared__ double ser_s;
     __shared__ uint64_t etab[32];
-    const int n = *pos_ptr + 1;
+    // blockIdx.z: the sequence of a batched decode step (as in k_attn_scores)
+    const int z = blockIdx.z;
+    att += (size_t)z * n_heads * max_seq;
+    V += z * kv_stride;
+    out += (size_t)z * n_heads * hd;
+    const int n = pos_ptr[z] + 1;
     if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
     if (n > QMH_PV_LONG) {
         if (n_kv != n_heads) return;  // grouped heads never get here (the launcher's bound on max_seq)
@@ -545,11 +557,37 @@ extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *
         const size_t lds_a = (size_t)640 + QMH_PV_CW * (640 + 4), lds_b = (size_t)QMH_PV_LONG + 2 * QMH_PV_CW * (128 + 4);
         hipLaunchKernelGGL(k_attn_pv_mha<640>, dim3(n_heads, grid.y), dim3(QMH_WG),
                            sizeof(float) * (lds_a > lds_b ? lds_a : lds_b), s, att, vcache, out, pos_ptr, n_heads,
-                           n_kv_heads, head_dim, max_seq);
+                           n_kv_heads, head_dim, max_seq, 0LL);
     }
     else if (group == 1) QMH_PV_GO(640, true);
     else if (group <= 8) QMH_PV_GO(640, false);
     else QMH_PV_GO(256, false);
 #undef QMH_PV_GO
+    return (int)hipGetLastError();
+}
+
+// The decode kernels over B sequences of a batched step (blockIdx.z = sequence): one query head per
+// kv head and head_dim 128, 64 or 48. Scores spread over (head, 64 positions) workgroups and P.V
+// over (head, 16 columns) ones, where the fused batched kernel reads a head's whole K and V in one
+// workgroup. Returns hipErrorNotSupported for other shapes.
+extern "C" int qmh_launch_attn_batch(const float *Q, const float *Kt, const float *V, long long kv_stride,
+                                     const int32_t *pos, float *att, float *out, int B, int n_heads, int n_kv,
+                                     int hd, int max_seq, float scale, void *stream) {
+    if (n_heads != n_kv || (hd != 128 && hd != 64 && hd != 48) || B < 1) return (int)hipErrorNotSupported;
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 gs(n_kv, (max_seq + QMH_SC_T - 1) / QMH_SC_T, B);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_attn_scores<128>, gs, dim3(QMH_SC_T), 0, s, Q, Kt, att, pos, n_heads, n_kv, hd, max_seq,
+                           scale, kv_stride);
+    else if (hd == 64)
+        hipLaunchKernelGGL(k_attn_scores<64>, gs, dim3(QMH_SC_T), 0, s, Q, Kt, att, pos, n_heads, n_kv, hd, max_seq,
+                           scale, kv_stride);
+    else
+        hipLaunchKernelGGL(k_attn_scores<48>, gs, dim3(QMH_SC_T), 0, s, Q, Kt, att, pos, n_heads, n_kv, hd, max_seq,
+                           scale, kv_stride);
+    const size_t lds_a = (size_t)640 + QMH_PV_CW * (640 + 4), lds_b = (size_t)QMH_PV_LONG + 2 * QMH_PV_CW * (128 + 4);
+    hipLaunchKernelGGL(k_attn_pv_mha<640>, dim3(n_heads, (hd + QMH_PV_CW - 1) / QMH_PV_CW, B), dim3(QMH_WG),
+                       sizeof(float) * (lds_a > lds_b ? lds_a : lds_b), s, att, V, out, pos, n_heads, n_kv, hd,
+                       max_seq, kv_stride);
     return (int)hipGetLastError();
 }

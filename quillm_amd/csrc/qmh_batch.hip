@@ -125,6 +125,7 @@ __global__ __launch_bounds__(QMH_WG) void k_bt_pv(const float *__restrict__ att,
 constexpr int BT_T = 1024;
 constexpr int BT_FC = 128;
 constexpr int BT_FUSE_MAX = 16384;
+constexpr int BT_DECODE_B = 3;
 __global__ __launch_bounds__(BT_T, 8) void k_bt_attn(const float *__restrict__ Q, const float *__restrict__ Kt,
                                                   const float *__restrict__ V, long long kv_stride,
                                                   const int32_t *__restrict__ pos_arr, float *out, int n_heads,
@@ -224,7 +225,14 @@ extern "C" int qmh_launch_bt_attention(const float *Q, const float *Kt, const fl
     if (B < 1 || hd < 4 || hd > 128 || hd % 4 || n_kv < 1 || n_heads % n_kv || max_pos < 0 || max_pos >= max_seq)
         return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    if (!split && max_pos < BT_FUSE_MAX) {
+    // up to BT_DECODE_B sequences: the single-sequence decode kernels with a sequence dimension (MHA
+    // shapes), whose workgroups each read a slice of a head's K or V instead of all of it
+    if (split == 0 && B <= BT_DECODE_B) {
+        const int rc = qmh_launch_attn_batch(Q, Kt, V, kv_stride, pos, att, out, B, n_heads, n_kv, hd, max_seq, scale,
+                                             stream);
+        if (rc != (int)hipErrorNotSupported) return rc;
+    }
+    if (split != 1 && max_pos < BT_FUSE_MAX) {
         const size_t lds = (size_t)(BT_FC * 128 + max_pos + 1) * sizeof(float);
         hipLaunchKernelGGL(k_bt_attn, dim3(n_heads, B), dim3(BT_T), lds, s, Q, Kt, V, kv_stride, pos, out, n_heads,
                            n_kv, hd, max_seq, scale);

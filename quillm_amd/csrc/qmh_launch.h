@@ -81,6 +81,12 @@ int qmh_launch_attn_scores_tile(const float *q, const float *kcache, float *att,
                                 int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
                        int n_kv_heads, int head_dim, int max_seq, void *stream);
+/* the decode attention kernels over B sequences of a batched step (MHA, head_dim 128/64/48; else
+ * hipErrorNotSupported): query Q[b][n_heads*hd], caches at Kt/V + b*kv_stride, position pos[b],
+ * scores att[b][n_heads][max_seq], out[b][n_heads*hd] */
+int qmh_launch_attn_batch(const float *Q, const float *Kt, const float *V, long long kv_stride, const int32_t *pos,
+                          float *att, float *out, int B, int n_heads, int n_kv, int hd, int max_seq, float scale,
+                          void *stream);
 /* ---- batched prefill (qmh_prefill.hip) ---- */
 enum { QMH_PF_STORE = 0, QMH_PF_ADD = 1, QMH_PF_QKV = 2, QMH_PF_SWIGLU = 3 };
 typedef struct {
@@ -135,9 +141,10 @@ int qmh_launch_pf_attention(const float *Q, const float *Kt, const float *V, flo
 /* attention of B independent sequences, one query each (src/model.c:127-156 per sequence): sequence b
  * at position pos[b] (device), query Q[b][n_heads*hd], caches Kt + b*kv_stride ([kvd][max_seq]) and
  * V + b*kv_stride ([max_seq][kvd]); att: scratch [B][n_heads][max_seq]; out[b][n_heads*hd].
- * max_pos: the largest pos[b] (sizes the grid and the LDS). split == 0: one fused kernel when
- * max_pos < 16384 (att unused), else three launches through att; split != 0: always three launches
- * (same results; kept selectable so both paths stay tested). */
+ * max_pos: the largest pos[b] (sizes the grid and the LDS). split == 0: up to 3 sequences of one query
+ * head per kv head and head_dim 128/64/48 the decode kernels with a sequence dimension (through att),
+ * else one fused kernel when max_pos < 16384 (att unused), else three launches through att;
+ * split == 1: always three launches; split == 2: the fused kernel when max_pos < 16384 */
 int qmh_launch_bt_attention(const float *Q, const float *Kt, const float *V, long long kv_stride, const int32_t *pos,
                             int max_pos, float *att, float *out, int B, int n_heads, int n_kv, int hd, int max_seq,
                             float scale, int split, void *stream);

@@ -115,14 +115,16 @@ def attention_reference(oracle, q, kt, v, n, n_kv, hd, scale):
 
 @pytest.mark.parametrize("n_heads,n_kv,hd,positions", [
     (4, 4, 64, [0, 127, 128, 129]),
+    (2, 2, 128, [639, 641, 1300]),
     (8, 2, 128, [1023, 1024, 1025, 5]),
     (6, 3, 96, [255, 700, 2047]),
     (2, 1, 4, [0, 1, 300]),
 ])
 def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positions):
-    """The fused attention kernel and the three-launch path it replaces up to 16384 positions give
-    the same bits, and both the float32 restatement's; positions straddle the V chunk (128) and
-    the thread count (1024)."""
+    """The fused attention kernel, the three-launch path it replaces up to 16384 positions and the
+    automatic choice (the decode kernels with a sequence dimension for up to 3 MHA sequences of
+    head_dim 128/64/48) give the same bits, and all the float32 restatement's; positions straddle
+    the V chunk (128), the thread count (1024) and the decode P.V's 640-position chunk."""
     import ctypes
     say("batch attention", n_heads, n_kv, hd, positions)
     L = gpu.load_library()
@@ -143,7 +145,7 @@ def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positio
         fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                               ctypes.c_void_p] + [ctypes.c_int] * 5 + [ctypes.c_float,
                                                                                       ctypes.c_int, ctypes.c_void_p]
-        for split in (0, 1):
+        for split in (2, 1, 0):
             o = gpu.DeviceBuffer(B * n_heads * hd * 4)
             rc = fn(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, kvd * S, bufs[3].ptr, int(pos.max()), att.ptr, o.ptr, B,
                     n_heads, n_kv, hd, S, float(scale), split, L.qmh_stream())
@@ -155,6 +157,7 @@ def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positio
         for b in bufs + [att]:
             b.free()
     assert np.array_equal(bits(outs[0]), bits(outs[1])), "fused and split paths differ"
+    assert np.array_equal(bits(outs[0]), bits(outs[2])), "fused path and the automatic choice differ"
     for b in range(B):
         want = attention_reference(oracle, q[b], kt[b], v[b], int(pos[b]) + 1, n_kv, hd, scale)
         assert np.array_equal(bits(outs[0][b]), bits(want)), f"sequence {b} (pos {pos[b]})"
@@ -164,8 +167,9 @@ def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positio
 def test_batch_forward_wide(gpu, oracle, tmp_path, wt):
     """The 7B layer shapes (4096 wide, hidden 11008, one layer, vocabulary 8192): the multi-token matvec
     gives each workgroup 2-3 tiles of QKV, Wo, W2 and the output, and runs W1|W3 (344 tiles) in LDS
-    rounds at 3 and 4 tokens, for both weight types (their slot widths differ). Per-sequence logits at
-    2, 3 and 4 sequences, mixed positions, bitwise the oracle's single-sequence forwards."""
+    rounds at 3 and 4 tokens, for both weight types (their slot widths differ); attention through the
+    decode kernels with a sequence dimension up to 3 sequences, the fused kernel at 4. Per-sequence
+    logits at 1-4 sequences, mixed positions, bitwise the oracle's single-sequence forwards."""
     say("batch wide", wt)
     cfg = gpu.QmhConfig(dim=4096, hidden_dim=11008, n_layers=1, n_heads=32, n_kv_heads=32, vocab_size=8192,
                         max_seq=16, rope_theta=10000.0, norm_eps=1e-5)
@@ -174,7 +178,7 @@ def test_batch_forward_wide(gpu, oracle, tmp_path, wt):
     rs = np.random.default_rng(3)
     with gpu.Model.load(path) as m:
         V = m.vocab
-        for B in (2, 3, 4):
+        for B in (1, 2, 3, 4):
             lens = [2 + i for i in range(B)]
             toks = [rs.integers(0, V, L).astype(np.int32) for L in lens]
             want = [oracle_logits(oracle, path, t) for t in toks]
