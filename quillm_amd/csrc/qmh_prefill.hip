@@ -568,13 +568,14 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;
     PfLane<NM, 1> ln;
     {
-        const int row = r0 + tok, grp = r0 + 4 * kq;  // A row; first D row
+        const int row = r0 + tok;  // the lane's A row
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             ln.a[m][0] = pf_slot0(a, row < a.rows_alloc ? row : 0, m) * CB + (WT == QMH_Q8 ? 8 : 4) * kq;
-            ln.s[m][0] = pf_slot0(a, grp < a.rows_alloc ? grp : 0, m);
+            ln.w[m][0] = pf_slot0(a, row < a.rows_alloc ? row : 0, m);
         }
     }
+    const uint32_t kmask = kq == 0 ? 0xffffu : 0u;  // lanes of k = 0..3
     ln.x = (uint32_t)tok * 32 + 8 * kq;
     ln.d = (uint32_t)tok;
     float s[NPAIR][NM];
@@ -589,39 +590,47 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 #pragma unroll
             for (int j = 0; j < PD; j++) {
                 const int jb = 8 * (k0 + j) + wave;
-                pf_load<WT, NM, 1, TT>(a, base + (jb < nr ? jb : nr - 1), ln, blk[j]);
+                pf_load<WT, NM, 1, TT, true>(a, base + (jb < nr ? jb : nr - 1), ln, blk[j]);
             }
 #pragma unroll
             for (int j = 0; j < PD; j++) {
                 const int jb = 8 * (k0 + j) + wave;
                 if (jb < nr) {  // uniform per wave
                     // every MFMA of the block first, each into its own registers, then the terms:
-                    // the multiplies overlap instead of each waiting for the previous results
+                    // the multiplies overlap instead of each waiting for the previous results. The
+                    // scale products dw * dx come from an f16 MFMA with the scales at k = 0, as in
+                    // k_pf_gemm (exact: a product of two fp16 values)
                     pf_v4i acc[NM][TT];
+                    pf_v4f pw[NM][TT];
+                    pf_v4h Bs[TT];
 #pragma unroll
-                    for (int m = 0; m < NM; m++) {
-                        const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
-#pragma unroll
-                        for (int tt = 0; tt < TT; tt++) {
-                            const pf_v4i z = {0, 0, 0, 0};
-                            acc[m][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[tt], z, 0, 0, 0);
-                        }
+                    for (int tt = 0; tt < TT; tt++) {
+                        const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)blk[j].dx[tt]) & kmask;
+                        Bs[tt] = __builtin_bit_cast(pf_v4h, make_uint2(h, 0u));
                     }
 #pragma unroll
                     for (int m = 0; m < NM; m++) {
-                        const uint2 sc = blk[j].sc[m][0];
-                        const float dw[4] = {qmh_h2f((uint16_t)(sc.x & 0xffffu)), qmh_h2f((uint16_t)(sc.x >> 16)),
-                                             qmh_h2f((uint16_t)(sc.y & 0xffffu)), qmh_h2f((uint16_t)(sc.y >> 16))};
+                        const long Am = WT == QMH_Q8 ? blk[j].A[m][0] : pf_q4_operand((uint32_t)blk[j].A[m][0]);
+                        const pf_v4h As = __builtin_bit_cast(pf_v4h, make_uint2(blk[j].wh[m][0] & kmask, 0u));
+#pragma unroll
+                        for (int tt = 0; tt < TT; tt++) {
+                            const pf_v4i z = {0, 0, 0, 0};
+                            const pf_v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+                            acc[m][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Am, blk[j].B[tt], z, 0, 0, 0);
+                            pw[m][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(As, Bs[tt], zf, 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
 #pragma unroll
                         for (int tt = 0; tt < TT; tt++) {
                             const int p = 16 * tt + tok;
                             if (p < P)
 #pragma unroll
                                 for (int e = 0; e < 4; e++)
-                                    T[(((size_t)m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
-                                        (float)acc[m][tt][e] * (dw[e] * blk[j].dx[tt]);
+                                    T[((m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
+                                        (float)acc[m][tt][e] * pw[m][tt][e];
                         }
-                    }
                 }
             }
         }
