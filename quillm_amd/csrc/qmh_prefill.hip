@@ -668,7 +668,7 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 // sum q x - 8 sum x, exact). They are built either from the Q8_0 image of k_pf_quant (its perm8
 // groups [e0 e2 e4 e6 e1 e3 e5 e7] give their first 4 bytes to the even half and the last 4 to the
 // odd half) or, for a plain input, straight from the f32 rows (bmv_records_f32).
-#define BMV_P 4
+#define BMV_P 3
 #define BMV_NT 512
 #define BMV_REC 48
 #define BMV_CH 4  // (row, token) pairs per thread: rows of a workgroup x tokens <= 4*BMV_NT
@@ -730,7 +730,8 @@ __device__ __forceinline__ void bmv_records_f32(const qmh_pf_args &a, uint8_t *r
     }
 }
 
-template <int WT>
+// MP: the largest token count P the instance serves (its per-token loop is unrolled MP times)
+template <int WT, int MP>
 __global__ __launch_bounds__(BMV_NT, 4) void k_bmv(qmh_pf_args a) {  // 4 waves per SIMD: two per CU
     constexpr int CB = WT == QMH_Q8 ? 32 : 16;  // code bytes per slot
     constexpr int NV = CB / 16;
@@ -812,7 +813,7 @@ __global__ __launch_bounds__(BMV_NT, 4) void k_bmv(qmh_pf_args a) {  // 4 waves 
                 if (j0 + u < nper) {  // uniform
                     const float dw = qmh_h2f((uint16_t)sc[u]);
 #pragma unroll
-                    for (int p = 0; p < BMV_P; p++)
+                    for (int p = 0; p < MP; p++)
                         if (p < P) {
                             const uint8_t *rp = smem + (size_t)((q0 + bcur) * P + p) * BMV_REC;
                             const int4 x0 = *(const int4 *)rp, x1 = *(const int4 *)(rp + 16);
@@ -939,8 +940,17 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
                 lds = rec + (size_t)bq * per_block;
             }
         }
-        if (a->dtype == QMH_Q4) hipLaunchKernelGGL(k_bmv<QMH_Q4>, dim3(G), dim3(BMV_NT), lds, s, b);
-        else hipLaunchKernelGGL(k_bmv<QMH_Q8>, dim3(G), dim3(BMV_NT), lds, s, b);
+#define BMV_GO(MP_)                                                                                    \
+    do {                                                                                                 \
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_bmv<QMH_Q4, MP_>), dim3(G), dim3(BMV_NT), lds, s, b); \
+        else hipLaunchKernelGGL((k_bmv<QMH_Q8, MP_>), dim3(G), dim3(BMV_NT), lds, s, b);                  \
+    } while (0)
+        // one instance for 1-2 tokens, one for 3 (the single-token instance was 2% slower at one
+        // sequence than the 2-token one)
+        static_assert(BMV_P == 3, "k_bmv instances for up to 3 tokens");
+        if (a->P <= 2) BMV_GO(2);
+        else BMV_GO(3);
+#undef BMV_GO
         return (int)hipGetLastError();
     }
     if (a->P <= 32) {  // decode-sized batches: the skinny matmul streams every weight once

@@ -167,7 +167,7 @@ def test_batch_attention_fused_and_split(gpu, oracle, n_heads, n_kv, hd, positio
 def test_batch_forward_wide(gpu, oracle, tmp_path, wt):
     """The 7B layer shapes (4096 wide, hidden 11008, one layer, vocabulary 8192): the multi-token matvec
     gives each workgroup 2-3 tiles of QKV, Wo, W2 and the output, and runs W1|W3 (344 tiles) in LDS
-    rounds at 3 and 4 tokens, for both weight types (their slot widths differ); attention through the
+    rounds at 3 tokens (the skinny matmul takes 4), for both weight types (their slot widths differ); attention through the
     decode kernels with a sequence dimension up to 3 sequences, the fused kernel at 4. Per-sequence
     logits at 1-4 sequences, mixed positions, bitwise the oracle's single-sequence forwards."""
     say("batch wide", wt)
