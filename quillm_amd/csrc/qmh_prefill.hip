@@ -546,7 +546,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
 // fit the LDS budget at this P: wave w takes blocks base + 8j + w in batches of PD (each batch's
 // loads all in flight, no barrier inside a round), takes each block's exact int32 dot for TT
 // token tiles from MFMAs with a zero accumulator, and stores the term (float)acc*(dw*dx) in LDS
-// at [matrix][block in round][row][token]; after the round one thread per (row, token) pair
+// at [matrix][block in round][token][row]; after the round one thread per (row, token) pair
 // extends that pair's serial chain over the round's blocks in order (the reference's order).
 // After the last round each pair runs the epilogue. Dynamic LDS: one round's terms, at most SK_LDS.
 #define SK_WG 512
@@ -625,11 +625,12 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
 #pragma unroll
                         for (int tt = 0; tt < TT; tt++) {
                             const int p = 16 * tt + tok;
-                            if (p < P)
+                            if (p < P) {  // rows 4*kq .. +3 of token p: one 16-byte store
+                                pf_v4f t;
 #pragma unroll
-                                for (int e = 0; e < 4; e++)
-                                    T[((m * rblk + jb) * 16 + 4 * kq + e) * P + p] =
-                                        (float)acc[m][tt][e] * pw[m][tt][e];
+                                for (int e = 0; e < 4; e++) t[e] = (float)acc[m][tt][e] * pw[m][tt][e];
+                                *(pf_v4f *)(T + ((m * rblk + jb) * P + p) * 16 + 4 * kq) = t;
+                            }
                         }
                 }
             }
@@ -641,7 +642,7 @@ __global__ __launch_bounds__(SK_WG) void k_sk_gemm(qmh_pf_args a) {
             if (p < P)
                 for (int jb = 0; jb < nr; jb++)  // the matrices' chains side by side, each in block order
 #pragma unroll
-                    for (int m = 0; m < NM; m++) s[k][m] = s[k][m] + T[(((size_t)m * rblk + jb) * 16 + row) * P + p];
+                    for (int m = 0; m < NM; m++) s[k][m] = s[k][m] + T[((m * rblk + jb) * P + p) * 16 + row];
         }
         __syncthreads();
     }
