@@ -89,6 +89,11 @@ int qmh_launch_attn_batch(const float *Q, const float *Kt, const float *V, long 
                           void *stream);
 /* ---- batched prefill (qmh_prefill.hip) ---- */
 enum { QMH_PF_STORE = 0, QMH_PF_ADD = 1, QMH_PF_QKV = 2, QMH_PF_SWIGLU = 3 };
+/* token counts up to this run the skinny matmul (every weight streamed once for all tokens), larger
+ * ones the tiled matmul */
+#ifndef QMH_PF_SKINNY_P
+#define QMH_PF_SKINNY_P 64
+#endif
 typedef struct {
     /* weight: tiled codes/scales as for the matvec; il: interleaved W1 | W3 tiles */
     int dtype;
@@ -108,7 +113,7 @@ typedef struct {
     float eps;
     /* epilogue: out0 row-major [P][ld0]; QKV: q -> out0, k -> out1 ([kvd][max_seq]), v -> out2 */
     int epi;
-    /* SWIGLU through the tiled matmul (P > 32): with qxc set, the output is written only as the next
+    /* SWIGLU through the tiled matmul (P > QMH_PF_SKINNY_P): with qxc set, the output is written only as the next
      * matmul's Q8_0 image, codes [nb][PP][32] (Q4_0 order when qperm8) and scales [nb][PP], instead of
      * out0 (the quantization the launcher would run on it, bit for bit) */
     int8_t *qxc;

@@ -541,7 +541,7 @@ __global__ __launch_bounds__(QMH_WG) void k_pf_gemm(qmh_pf_args a) {
         }
 }
 
-// Skinny matmul for decode-sized batches (P <= 16*TT tokens): one workgroup per 16-row group
+// Skinny matmul for decode-sized batches (P <= 16*TT tokens, TT <= 4): one workgroup per 16-row group
 // streams every block of its rows once for all tokens. The blocks pass in rounds of as many as
 // fit the LDS budget at this P: wave w takes blocks base + 8j + w in batches of PD (each batch's
 // loads all in flight, no barrier inside a round), takes each block's exact int32 dot for TT
@@ -907,7 +907,7 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     // the image output exists only in the tiled matmul's SwiGLU epilogue (more than 32 tokens)
-    if (a->qxc && (a->epi != QMH_PF_SWIGLU || !a->qxd || a->P <= 32 || PF_NR != 2)) return (int)hipErrorInvalidValue;
+    if (a->qxc && (a->epi != QMH_PF_SWIGLU || !a->qxd || a->P <= QMH_PF_SKINNY_P || PF_NR != 2)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     if (a->xf && (a->nxf < 1 || a->nxf > 32 * a->nb || a->ldxf < a->nxf)) return (int)hipErrorInvalidValue;
     // the multi-token matvec when one tile's terms fit its LDS with the records. It quantizes a plain
@@ -954,7 +954,7 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
 #undef BMV_GO
         return (int)hipGetLastError();
     }
-    if (a->P <= 32) {  // decode-sized batches: the skinny matmul streams every weight once
+    if (a->P <= QMH_PF_SKINNY_P) {  // decode-sized batches: the skinny matmul streams every weight once
         const dim3 g((a->rows + 15) / 16);
         const int nm = a->il ? 2 : 1;
         const size_t lds = (size_t)sk_round(a->nb, nm, a->P) * nm * 16 * a->P * sizeof(float);
@@ -972,9 +972,12 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
         } else if (a->P <= 16) {
             if (a->il) SK_LAUNCH(2, 1, 8);
             else SK_LAUNCH(1, 1, 6);
-        } else {
+        } else if (a->P <= 32) {
             if (a->il) SK_LAUNCH(2, 2, 4);
             else SK_LAUNCH(1, 2, 8);
+        } else {  // 33..64 tokens: a round holds 16 (W1 | W3) or 32 blocks, 2 or 4 per wave; 2 ahead
+            if (a->il) SK_LAUNCH(2, 4, 2);
+            else SK_LAUNCH(1, 4, 2);
         }
 #undef SK_LAUNCH
         return (int)hipGetLastError();

@@ -954,8 +954,9 @@ static int pf_layer(qmh_model *m, int l, int P, int pos, const pf_seqs *bt, hipS
     a.epi = QMH_PF_SWIGLU;
     a.out0 = m->d_pf_hb;
     a.ld0 = H;
-    /* past 32 tokens (the tiled matmul) hb is written only as W2's quantized image */
-    const int hb_image = P > 32;
+    /* past the skinny matmul's token counts (the tiled matmul) hb is written only as W2's quantized
+     * image */
+    const int hb_image = P > QMH_PF_SKINNY_P;
     if (hb_image) {
         a.qxc = m->d_pf_xc2;
         a.qxd = m->d_pf_xd2;

@@ -30,7 +30,8 @@ def oracle_logits(oracle, path, toks):
 
 
 @pytest.mark.parametrize("shape,wt,B", [("small", "q8_0", 3), ("small", "q4_0", 5), ("gqa", "q4_0", 4),
-                                        ("gqa48", "q4_0", 2), ("mha", "q8_0", 1), ("odd", "q4_0", 3)])
+                                        ("gqa48", "q4_0", 2), ("mha", "q8_0", 1), ("odd", "q4_0", 3),
+                                        ("small", "q4_0", 40), ("odd", "q8_0", 64)])
 def test_batch_forward_matches_single_sequences(gpu, oracle, small_models, shape, wt, B):
     say("batch", shape, wt, B)
     path = small_models[(shape, wt)]

@@ -191,8 +191,9 @@ def test_batched_prefill_head_dims(gpu, tmp_path, hd, n_heads, n_kv, wt):
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
     """W2's input rows of 202 values (n % 4 == 2): the activation quantizer's per-value path
-    instead of its 16-byte loads (the skinny matmul at 20 tokens), beside the multi-token matvec's
-    own quantization (3 tokens) and W1|W3's image epilogue (40), against sequential forwards.
+    instead of its 16-byte loads (the skinny matmul at 20 and 33 tokens: two and four token tiles),
+    beside the multi-token matvec's own quantization (3 tokens) and W1|W3's image epilogue (70: the
+    tiled matmul), against sequential forwards.
     (The batched prefill needs head_dim % 4 == 0, so dim % 4 == 0.)"""
     import os
 
@@ -200,7 +201,7 @@ def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
     cfg = gpu.QmhConfig(dim=96, hidden_dim=202, n_layers=2, n_heads=8, n_kv_heads=4, vocab_size=300, max_seq=128,
                         rope_theta=10000.0, norm_eps=1e-5)
     gpu.gen_model(path, cfg, wt, seed=33, threads=4)
-    chunks = [gpu.prompt_ids(n, 300, seed=20 + n) for n in (40, 20, 3)]
+    chunks = [gpu.prompt_ids(n, 300, seed=20 + n) for n in (70, 33, 20, 3)]
     runs = []
     for seq in (False, True):
         if seq:
