@@ -899,8 +899,11 @@ __global__ __launch_bounds__(BMV_NT, 4) void k_bmv(qmh_pf_args a) {  // 4 waves 
 
 // Wave shape of the matmuls (timed on MI355X at P = 512 over the 7B shapes): 2 row tiles x 4
 // token tiles per wave, 2 blocks loaded ahead. Fewer tiles per wave issue more loads per MFMA;
-// more leave too few waves to cover the latency at P = 512.
-enum { PF_NR = 2, PF_TW = 4, PF_PD = 2 };
+// more leave too few waves to cover the latency at P = 512. W1 | W3 loads 1 block ahead: that
+// holds it to 166 VGPRs, three waves per SIMD, so its 2752 wave tiles at P = 512 (7B shapes) run
+// in one round of 3072 slots instead of 1.34 rounds of 2048 (20.45 -> 20.02 ms per 512-token
+// prefill); the other matrices lose at depth 1 (23.5 ms with every one there).
+enum { PF_NR = 2, PF_TW = 4, PF_PD = 2, PF_PD13 = 1 };
 
 extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
@@ -986,8 +989,8 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     // PP-token activation buffer
     const dim3 g((a->P + 16 * PF_TW - 1) / (16 * PF_TW), (a->rows + 64 * PF_NR - 1) / (64 * PF_NR));
     if (a->il) {
-        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 2, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
-        else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 2, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
+        if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 2, PF_NR, PF_TW, PF_PD13>), g, dim3(QMH_WG), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 2, PF_NR, PF_TW, PF_PD13>), g, dim3(QMH_WG), 0, s, *a);
     } else {
         if (a->dtype == QMH_Q4) hipLaunchKernelGGL((k_pf_gemm<QMH_Q4, 1, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
         else hipLaunchKernelGGL((k_pf_gemm<QMH_Q8, 1, PF_NR, PF_TW, PF_PD>), g, dim3(QMH_WG), 0, s, *a);
