@@ -909,7 +909,7 @@ extern "C" int qmh_launch_pf_gemm(const qmh_pf_args *a, void *stream) {
     if (a->PP % 128 || a->P > a->PP || a->P < 1 || a->nb < 1) return (int)hipErrorInvalidValue;
     if ((a->epi == QMH_PF_SWIGLU) != (a->il != 0)) return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
-    // the image output exists only in the tiled matmul's SwiGLU epilogue (more than 32 tokens)
+    // the image output exists only in the tiled matmul's SwiGLU epilogue (more than QMH_PF_SKINNY_P tokens)
     if (a->qxc && (a->epi != QMH_PF_SWIGLU || !a->qxd || a->P <= QMH_PF_SKINNY_P || PF_NR != 2)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     if (a->xf && (a->nxf < 1 || a->nxf > 32 * a->nb || a->ldxf < a->nxf)) return (int)hipErrorInvalidValue;

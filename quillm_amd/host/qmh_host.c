@@ -390,7 +390,7 @@ struct qmh_model {
     int pf_ok, pf_cap, pf_pp;
     int32_t *d_pf_tok, *h_pf_tok;
     float *d_pf_x, *d_pf_xb, *d_pf_q, *d_pf_hb, *d_pf_att, *d_pf_logits, *d_pf_xd;
-    int8_t *d_pf_xc2; /* W2's input image, written by W1|W3's epilogue past 32 tokens */
+    int8_t *d_pf_xc2; /* W2's input image, written by W1|W3's epilogue past QMH_PF_SKINNY_P tokens */
     float *d_pf_xd2;
     int8_t *d_pf_xc;
 };
