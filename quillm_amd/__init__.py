@@ -238,7 +238,7 @@ class Model:
                                                 out.ctypes.data), "model_sample")
         return out[:n_steps]
 
-    STAGES = {"qkv": 0, "wo": 1, "w13": 2, "w2": 3, "output": 4, "attn_scores": 5, "attn_pv": 6}
+    STAGES = {"qkv": 0, "wo": 1, "w13": 2, "w2": 3, "output": 4, "attn_scores": 5, "attn_pv": 6, "attn": 7}
 
     def time_stage(self, stage: str, iters: int, pos: int):
         """(ms per launch, weight bytes per launch) of one decode-step stage at position pos, from HIP events."""

@@ -386,71 +386,25 @@ __device__ __forceinline__ void pv_mha_long(const float *__restrict__ s0, const 
     if (chain && i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
 }
 
-// One workgroup per (query head, 16 output columns), head_dim a multiple of 4: its V is that of the
-// head's kv head h / (n_heads / n_kv) (the query heads of a group read it from L2). Contexts of up
-// to TC positions run here; up to QMH_PV_LONG, pv_mha_long; longer ones, only when every kv head
-// serves one query head (the launcher keeps grouped heads within QMH_PV_LONG), attn_pv_chunks. Same
-// sums in the same order as the reference, laid out for a shorter critical path:
-//   * V is read as float4 (4 columns of one position per thread);
-//   * the softmax exponentials e_t stay in LDS (P) from the statistics to the products, and the
-//     serial fallback of the sum reads them there;
-//   * each reduction takes one barrier (its own LDS buffer);
-//   * the products p_t*v_t are staged in pieces of 128 positions: while the chain lanes (the
-//     first 16 threads, one output column each) add piece j, the other waves stage piece j+1.
+// k_attn_pv_mha's path for contexts of up to TC positions, after its loads: the softmax statistics
+// over the head's n scores (sv[k] holds position tid + k*QMH_WG) and the V sum of this workgroup's
+// 16 columns (vv[k] holds position k*64 + tid/4, columns i0 + 4*(tid%4) .. +3). x0p points to the
+// score of position 0 (the reference's max scan starts from it). etv: expf's table entry tid (< 32).
 template <int TC>
-__global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict__ att, const float *__restrict__ V,
-                                                        float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
-                                                        int n_kv, int hd, int max_seq, long long kv_stride) {
+__device__ __forceinline__ void pv_short(const float (&sv)[(TC + QMH_WG - 1) / QMH_WG],
+                                         float4 (&vv)[TC * QMH_PV_CW / 4 / QMH_WG], uint64_t etv, const float *x0p,
+                                         int n, int h, int i0, int hd, float *__restrict__ out, float *pv_smem) {
     constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
     constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
     constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
     constexpr int PC = 128;                          // positions per staged piece
-    static_assert(QMH_PV_CW == 16 && TC % PC == 0 && (TC * QMH_PV_CW / 4) % QMH_WG == 0, "whole pieces, whole loads");
-    static_assert(PC * QMH_PV_CW / 4 == 2 * QMH_WG, "a piece is two float4 loads of every thread");
-    extern __shared__ __align__(16) float pv_smem[];
     float *P = pv_smem;       // [TC] exponentials e_t
     float *Vs = pv_smem + TC; // [CW][VS] products, transposed
     __shared__ float wmax[QMH_WG / 64];
     __shared__ double wsum[QMH_WG / 64];
     __shared__ double ser_s;
     __shared__ uint64_t etab[32];
-    // blockIdx.z: the sequence of a batched decode step (as in k_attn_scores)
-    const int z = blockIdx.z;
-    att += (size_t)z * n_heads * max_seq;
-    V += z * kv_stride;
-    out += (size_t)z * n_heads * hd;
-    const int n = pos_ptr[z] + 1;
-    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
-    if (n > QMH_PV_LONG) {
-        if (n_kv != n_heads) return;  // grouped heads never get here (the launcher's bound on max_seq)
-        attn_pv_chunks<TC, true>(att, V, out, n, n_heads, n_heads, hd, max_seq);
-        return;
-    }
-    if (n > TC) {
-        pv_mha_long<3>(att + (size_t)blockIdx.x * max_seq, V, out, n, blockIdx.x, blockIdx.x / (n_heads / n_kv),
-                       blockIdx.y * QMH_PV_CW, hd, hd * n_kv, pv_smem, pv_smem + QMH_PV_LONG);
-        return;
-    }
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int h = blockIdx.x, kvh = h / (n_heads / n_kv), i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
-    const float *s0 = att + (size_t)h * max_seq;
-    // loads: expf's table (oldest, so storing it to LDS below waits for nothing else), the head's
-    // scores, then the V float4s (position k*64 + tid/4, columns c .. c+3; columns past hd
-    // re-read the last whole float4 and are never stored)
-    const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
-    float sv[SK];
-#pragma unroll
-    for (int k = 0; k < SK; k++) {
-        const int t = tid + k * QMH_WG;
-        sv[k] = s0[t < n ? t : 0];
-    }
-    const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
-    float4 vv[L4];
-#pragma unroll
-    for (int k = 0; k < L4; k++) {
-        const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
-        vv[k] = *(const float4 *)(V + (size_t)tcl * kvd + (size_t)kvh * hd + cc);
-    }
     // softmax statistics (src/ops.c:100-112): max (NaN never wins; a NaN at x[0] stays),
     // e_t = expf(x_t - max) kept in P, the double sum as a tree checked against the serial order
     if (tid < 32) etab[tid] = etv;  // published by the max's barrier
@@ -464,7 +418,8 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     m = wmax[0];
 #pragma unroll
     for (int w = 1; w < QMH_WG / 64; w++) m = fmaxf(m, wmax[w]);
-    if (s0[0] != s0[0]) m = s0[0];
+    const float x0 = *x0p;
+    if (x0 != x0) m = x0;
     double sum = 0.0;
 #pragma unroll
     for (int k = 0; k < SK; k++) {
@@ -539,6 +494,266 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
         __syncthreads();
     }
     if (chain && i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
+}
+
+// One workgroup per (query head, 16 output columns), head_dim a multiple of 4: its V is that of the
+// head's kv head h / (n_heads / n_kv) (the query heads of a group read it from L2). Contexts of up
+// to TC positions run here; up to QMH_PV_LONG, pv_mha_long; longer ones, only when every kv head
+// serves one query head (the launcher keeps grouped heads within QMH_PV_LONG), attn_pv_chunks. Same
+// sums in the same order as the reference, laid out for a shorter critical path:
+//   * V is read as float4 (4 columns of one position per thread);
+//   * the softmax exponentials e_t stay in LDS (P) from the statistics to the products, and the
+//     serial fallback of the sum reads them there;
+//   * each reduction takes one barrier (its own LDS buffer);
+//   * the products p_t*v_t are staged in pieces of 128 positions: while the chain lanes (the
+//     first 16 threads, one output column each) add piece j, the other waves stage piece j+1.
+template <int TC>
+__global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict__ att, const float *__restrict__ V,
+                                                        float *__restrict__ out, const int32_t *pos_ptr, int n_heads,
+                                                        int n_kv, int hd, int max_seq, long long kv_stride) {
+    constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
+    constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
+    static_assert(QMH_PV_CW == 16 && TC % 128 == 0 && (TC * QMH_PV_CW / 4) % QMH_WG == 0, "whole pieces, whole loads");
+    extern __shared__ __align__(16) float pv_smem[];
+    // blockIdx.z: the sequence of a batched decode step (as in k_attn_scores)
+    const int z = blockIdx.z;
+    att += (size_t)z * n_heads * max_seq;
+    V += z * kv_stride;
+    out += (size_t)z * n_heads * hd;
+    const int n = pos_ptr[z] + 1;
+    if (n < 1 || n > max_seq) return;  // stale position in device memory: touch nothing
+    if (n > QMH_PV_LONG) {
+        if (n_kv != n_heads) return;  // grouped heads never get here (the launcher's bound on max_seq)
+        attn_pv_chunks<TC, true>(att, V, out, n, n_heads, n_heads, hd, max_seq);
+        return;
+    }
+    if (n > TC) {
+        pv_mha_long<3>(att + (size_t)blockIdx.x * max_seq, V, out, n, blockIdx.x, blockIdx.x / (n_heads / n_kv),
+                       blockIdx.y * QMH_PV_CW, hd, hd * n_kv, pv_smem, pv_smem + QMH_PV_LONG);
+        return;
+    }
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x, kvh = h / (n_heads / n_kv), i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
+    const float *s0 = att + (size_t)h * max_seq;
+    // loads: expf's table (oldest, so storing it to LDS below waits for nothing else), the head's
+    // scores, then the V float4s (position k*64 + tid/4, columns c .. c+3; columns past hd
+    // re-read the last whole float4 and are never stored)
+    const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
+    float sv[SK];
+#pragma unroll
+    for (int k = 0; k < SK; k++) {
+        const int t = tid + k * QMH_WG;
+        sv[k] = s0[t < n ? t : 0];
+    }
+    const int c = i0 + 4 * (tid & 3), cc = c <= hd - 4 ? c : hd - 4;
+    float4 vv[L4];
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
+        vv[k] = *(const float4 *)(V + (size_t)tcl * kvd + (size_t)kvh * hd + cc);
+    }
+    pv_short<TC>(sv, vv, etv, s0, n, h, i0, hd, out, pv_smem);
+}
+
+// ============================================================================ one launch per step
+
+// The decode step's whole attention in one launch, for contexts of up to QMH_AF_TC positions:
+// workgroup (cg, h) of grid (head_dim/16, n_heads) owns query head h's output columns 16*cg ..
+// +15 (as k_attn_pv_mha) and computes the scores of a slice of the head's positions,
+// [cg*sp, cg*sp + sp) with sp = ceil(n / (head_dim/16)) rounded up to 4. Its K slice arrives as
+// float4s of 4 positions of one dimension (all in flight together), is staged in LDS as rows of
+// head_dim + 4 floats (one position per row), and one lane per position runs the score's serial
+// chain over head_dim. The scores go to attp[h][t] as 64-bit words (score bits | epoch << 32)
+// through agent-scope atomic stores; every workgroup of the head then loads the head's n words
+// with agent-scope atomic loads until each carries this launch's epoch, and runs k_attn_pv_mha's
+// statistics and V sum on them. A word is written and read whole, so a value is taken only with
+// the epoch it was stored with: the exchange needs no barrier and no fence. The epoch of layer l is
+// sync[0]*n_layers + l + 1; sync[0] counts decode steps (k_embed adds one per step), so no two
+// launches of a step, nor of two steps, share one, and attp holds only older epochs when a launch
+// starts. Every wait is bounded: past `spin` polls the workgroup sets sync[1] (which the host
+// reports as an error) and goes on. skew (0 in use) makes the readers wait for an epoch nobody
+// writes, so that a test can run the bounded wait to its end from the host. The head's workgroups are consecutive in dispatch order
+// (blockIdx.x fastest) and the host launches at most as many workgroups as the device holds at once.
+#define QMH_AF_TC 640
+#define QMH_AF_SPIN (1u << 16)
+template <int HD>
+__global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ Kt,
+                                                       const float *__restrict__ V, float *__restrict__ out,
+                                                       uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync,
+                                                       int n_heads, int n_kv, int max_seq, float scale, int layer,
+                                                       int n_layers, uint32_t spin, uint32_t skew) {
+    constexpr int TC = QMH_AF_TC, CW = QMH_PV_CW, NCG = HD / CW;
+    constexpr int SPM = ((TC + NCG - 1) / NCG + 3) / 4 * 4;          // most positions of one slice
+    constexpr int KS = HD + 4;                                       // LDS row stride of the K slice
+    constexpr int KL4 = (SPM / 4 * HD + QMH_WG - 1) / QMH_WG;        // float4 K loads per thread
+    constexpr int L4 = TC * CW / 4 / QMH_WG, SK = (TC + QMH_WG - 1) / QMH_WG;
+    static_assert(HD % CW == 0 && SPM <= QMH_WG, "whole column groups; one chain lane per position");
+    extern __shared__ __align__(16) float af_smem[];
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float x0s;
+    const int n = *pos_ptr + 1;
+    if (n < 1 || n > TC || n > max_seq) {  // the host takes longer contexts elsewhere: flag a stray launch
+        if (n > TC && n <= max_seq && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+            __hip_atomic_store(sync + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int tid = threadIdx.x;
+    const int cg = blockIdx.x, h = blockIdx.y, kvh = h / (n_heads / n_kv), kvd = HD * n_kv, i0 = cg * CW;
+    const uint32_t ep = sync[0] * (uint32_t)n_layers + (uint32_t)layer + 1u, want = ep + skew;
+    const int sp = ((n + NCG - 1) / NCG + 3) & ~3, p0 = cg * sp;
+    const int np = (n - p0 < sp ? n - p0 : sp) > 0 ? (n - p0 < sp ? n - p0 : sp) : 0;  // positions of the slice
+    const int np4 = (np + 3) >> 2, np4d = np4 > 0 ? np4 : 1;
+    // loads: q, the K slice (element e: dimension e / np4, positions p0 + 4*(e % np4) .. +3, clamped
+    // to a whole float4 inside the cache), expf's table, then V as k_attn_pv_mha
+    float4 q4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (tid < HD / 4) q4 = ((const float4 *)(q + (size_t)h * HD))[tid];
+    const float *kb = Kt + (size_t)kvh * HD * max_seq;
+    float4 kv[KL4];
+#pragma unroll
+    for (int k = 0; k < KL4; k++) {
+        const int e = k * QMH_WG + tid, d = e / np4d < HD ? e / np4d : HD - 1;
+        const int t = p0 + 4 * (e % np4d), tc = t <= max_seq - 4 ? t : max_seq - 4;
+        kv[k] = qmh_ld_nt4(kb + (size_t)d * max_seq + tc);
+    }
+    const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
+    // V (position k*64 + tid/4, columns c .. c+3), loaded non-temporally after K has arrived: loads
+    // issued together with K's delay it, and a wave that issues loads before its chain stalls in
+    // its chain. The waves without chain lanes issue theirs at once, the others after their chains.
+    const int c = i0 + 4 * (tid & 3), cc = c <= HD - 4 ? c : HD - 4;
+    float4 vv[L4];
+    auto vload = [&] {
+#pragma unroll
+        for (int k = 0; k < L4; k++) {
+            const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
+            vv[k] = qmh_ld_nt4(V + (size_t)tcl * kvd + (size_t)kvh * HD + cc);
+        }
+    };
+    // the slice in LDS, row r = position p0 + r
+    float *kt = af_smem;
+    if (tid < HD / 4) ((float4 *)qs)[tid] = q4;
+#pragma unroll
+    for (int k = 0; k < KL4; k++) {
+        const int e = k * QMH_WG + tid;
+        if (e < np4 * HD) {
+            const int d = e / np4d, r = 4 * (e % np4d);
+            kt[(r + 0) * KS + d] = kv[k].x;
+            kt[(r + 1) * KS + d] = kv[k].y;
+            kt[(r + 2) * KS + d] = kv[k].z;
+            kt[(r + 3) * KS + d] = kv[k].w;
+        }
+    }
+    __syncthreads();
+    // wave-uniform: does this wave hold chain lanes?
+    const bool chain_wave = (tid & ~63) < np;
+    if (!chain_wave) vload();
+    // scores: s = +0; s = s + q[i]*k[i] in dimension order, times scale (src/model.c:142-146); the
+    // row and q are read from LDS eight float4s ahead of their products
+    uint64_t *row = attp + (size_t)h * max_seq;
+    if (tid < np) {
+        const float4 *kr = (const float4 *)(kt + tid * KS), *qr = (const float4 *)qs;
+        float sc = 0.0f;
+#pragma unroll
+        for (int i0 = 0; i0 < HD / 4; i0 += 8) {
+            float4 kk[8], qq[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (i0 + i < HD / 4) {
+                    kk[i] = kr[i0 + i];
+                    qq[i] = qr[i0 + i];
+                }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i0 + i >= HD / 4) break;
+                sc = sc + qq[i].x * kk[i].x;
+                sc = sc + qq[i].y * kk[i].y;
+                sc = sc + qq[i].z * kk[i].z;
+                sc = sc + qq[i].w * kk[i].w;
+            }
+        }
+        sc = sc * scale;
+        __hip_atomic_store(row + p0 + tid, ((uint64_t)ep << 32) | __float_as_uint(sc), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the head's n scores, each once it carries this launch's epoch (the first loads go out before a
+    // chain wave's V loads, so waiting for them does not wait for V)
+    uint64_t w[SK];
+#pragma unroll
+    for (int k = 0; k < SK; k++) {
+        const int t = tid + k * QMH_WG;
+        w[k] = t < n ? __hip_atomic_load(row + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)want << 32;
+    }
+    if (chain_wave) vload();
+    for (uint32_t it = 0;; it++) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < SK; k++) ok &= (uint32_t)(w[k] >> 32) == want;
+        if (ok) break;
+        if (it >= spin) {
+            __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int k = 0; k < SK; k++) {
+            const int t = tid + k * QMH_WG;
+            if ((uint32_t)(w[k] >> 32) != want)
+                w[k] = __hip_atomic_load(row + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    float sv[SK];
+#pragma unroll
+    for (int k = 0; k < SK; k++) sv[k] = __uint_as_float((uint32_t)w[k]);
+    if (tid == 0) x0s = sv[0];
+    __syncthreads();  // the K slice is dead: its LDS is the V sum's from here
+    pv_short<TC>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
+}
+
+// dynamic LDS bytes of k_attn_fused<HD>: the larger of the K slice and the V sum's buffers
+static size_t af_lds_bytes(int hd) {
+    const int ncg = hd / QMH_PV_CW, spm = ((QMH_AF_TC + ncg - 1) / ncg + 3) / 4 * 4;
+    const size_t kslice = (size_t)spm * (hd + 4), pv = (size_t)QMH_AF_TC + QMH_PV_CW * (QMH_AF_TC + 4);
+    return sizeof(float) * (kslice > pv ? kslice : pv);
+}
+
+extern "C" int qmh_attn_fused_max_n(void) { return QMH_AF_TC; }
+
+// 1 when k_attn_fused takes the shape: head_dim 48, 64 or 128, max_seq a whole number of float4s, and
+// no more workgroups than the device holds at once (every head's workgroups run together); else 0
+extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
+    if ((head_dim != 128 && head_dim != 64 && head_dim != 48) || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 ||
+        n_heads % n_kv_heads)
+        return 0;
+    int dev = 0, ncu = 0, per = 0;
+    const void *k = head_dim == 128 ? (const void *)k_attn_fused<128>
+                    : head_dim == 64 ? (const void *)k_attn_fused<64> : (const void *)k_attn_fused<48>;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, QMH_WG, af_lds_bytes(head_dim)) != hipSuccess)
+        return 0;
+    return (long long)(head_dim / QMH_PV_CW) * n_heads <= (long long)per * ncu;
+}
+
+// the caller has checked qmh_attn_fused_supported for the shape; stall != 0 (tests only): the
+// readers wait for an epoch nobody writes, for 64 polls
+extern "C" int qmh_launch_attn_fused(const float *q, const float *kcache, const float *vcache, float *out,
+                                     uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync, int n_heads,
+                                     int n_kv_heads, int head_dim, int max_seq, float scale, int layer, int n_layers,
+                                     int stall, void *stream) {
+    if ((head_dim != 128 && head_dim != 64 && head_dim != 48) || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 ||
+        n_heads % n_kv_heads)
+        return (int)hipErrorNotSupported;
+    const dim3 grid(head_dim / QMH_PV_CW, n_heads);
+    const size_t lds = af_lds_bytes(head_dim);
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t spin = stall ? 64u : QMH_AF_SPIN, skew = stall ? 1u : 0u;
+#define QMH_AF(HD)                                                                                             \
+    hipLaunchKernelGGL(k_attn_fused<HD>, grid, dim3(QMH_WG), lds, s, q, kcache, vcache, out, attp, pos_ptr, sync, \
+                       n_heads, n_kv_heads, max_seq, scale, layer, n_layers, spin, skew)
+    if (head_dim == 128) QMH_AF(128);
+    else if (head_dim == 64) QMH_AF(64);
+    else QMH_AF(48);
+#undef QMH_AF
+    return (int)hipGetLastError();
 }
 
 extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *out, const int32_t *pos_ptr,

@@ -12,6 +12,14 @@
 
 #define QMH_WG 256  // threads per workgroup for the streaming kernels (4 wave64)
 
+// a 16-byte-aligned float4 loaded non-temporally (data read once per step, e.g. the KV cache: it
+// should not evict the code and the small vectors the next kernels read from L2)
+typedef float qmh_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 qmh_ld_nt4(const float *p) {
+    const qmh_v4f v = __builtin_nontemporal_load((const qmh_v4f *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // fp16 bits -> float. v_cvt_f32_f16 is exact for every finite half, subnormals included
 // (fp16 denormals are on by default on gfx9); reference src/fp16.c:6-31.
 __device__ __forceinline__ float qmh_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }

@@ -71,8 +71,9 @@ int qmh_matvec_max_cols(int norm);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
 int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
 
+/* step_ctr (may be NULL): a decode-step counter the kernel adds one to (k_attn_fused's epochs) */
 int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tok_ptr, float *x,
-                     void *stream);
+                     uint32_t *step_ctr, void *stream);
 int qmh_launch_attn_scores(const float *q, const float *kcache, float *att, const int32_t *pos_ptr, int n_heads,
                            int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 /* the same scores for a kv head serving several query heads: K tile in LDS (head_dim 48, 64 or
@@ -81,6 +82,15 @@ int qmh_launch_attn_scores_tile(const float *q, const float *kcache, float *att,
                                 int n_kv_heads, int head_dim, int max_seq, float scale, void *stream);
 int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const int32_t *pos_ptr, int n_heads,
                        int n_kv_heads, int head_dim, int max_seq, void *stream);
+/* a decode step's attention in one launch (k_attn_fused) for contexts of up to qmh_attn_fused_max_n()
+ * positions: scores exchanged between a head's workgroups as epoch-tagged words in attp
+ * [n_heads][max_seq] (zeroed at allocation); sync[0] counts decode steps (qmh_launch_embed),
+ * sync[1] != 0 reports a bounded wait that ran out (or a launch past the context limit) */
+int qmh_attn_fused_max_n(void);
+int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq);
+int qmh_launch_attn_fused(const float *q, const float *kcache, const float *vcache, float *out, uint64_t *attp,
+                          const int32_t *pos_ptr, uint32_t *sync, int n_heads, int n_kv_heads, int head_dim,
+                          int max_seq, float scale, int layer, int n_layers, int stall, void *stream);
 /* the decode attention kernels over B sequences of a batched step (MHA, head_dim 128/64/48; else
  * hipErrorNotSupported): query Q[b][n_heads*hd], caches at Kt/V + b*kv_stride, position pos[b],
  * scores att[b][n_heads][max_seq], out[b][n_heads*hd] */

@@ -15,7 +15,8 @@
 
 // x = dequantised row `token` of tok_embd (src/model.c:162 -> src/quant.c:65-101)
 __global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, int vocab, const int32_t *tok_ptr,
-                        float *x) {
+                        float *x, uint32_t *step_ctr) {
+    if (step_ctr && blockIdx.x == 0 && threadIdx.x == 0) step_ctr[0] += 1u;
     const int tok = *tok_ptr;
     if (tok < 0 || tok >= vocab) return;  // stale token in device memory: read nothing
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) {
@@ -37,9 +38,9 @@ __global__ void k_embed(const uint8_t *__restrict__ E, int dtype, int dim, int v
 }
 
 extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int vocab, const int32_t *tok_ptr,
-                                float *x, void *stream) {
+                                float *x, uint32_t *step_ctr, void *stream) {
     hipLaunchKernelGGL(k_embed, dim3((dim + 255) / 256), dim3(256), 0, (hipStream_t)stream, tok_embd, dtype, dim,
-                       vocab, tok_ptr, x);
+                       vocab, tok_ptr, x, step_ctr);
     return (int)hipGetLastError();
 }
 

@@ -385,6 +385,15 @@ struct qmh_model {
     float *h_logits;   /* pinned [vocab] */
     hipGraph_t graph_fwd, graph_greedy;
     hipGraphExec_t exec_fwd, exec_greedy;
+    /* the same steps with the attention in one launch (k_attn_fused), for positions below
+     * qmh_attn_fused_max_n() when af_ok */
+    hipGraph_t graph_fwd_af, graph_greedy_af;
+    hipGraphExec_t exec_fwd_af, exec_greedy_af;
+    int af_ok;
+    int af_stall;      /* QMH_AF_FORCE_STALL (tests): the one-launch attention's waits run out */
+    uint64_t *d_attp;  /* [n_heads][max_seq] epoch-tagged scores of k_attn_fused */
+    uint32_t *d_sync;  /* [0] decode steps (k_embed), [1] k_attn_fused's wait status */
+    uint32_t *h_sync;  /* pinned copy of d_sync[1] */
     int use_graph; /* 0 when QMH_NO_GRAPH is set: the same kernels, enqueued one by one (profiling) */
     /* batched prefill (every matrix quantized): up to pf_cap tokens per pass, padded to pf_pp */
     int pf_ok, pf_cap, pf_pp;
@@ -396,7 +405,7 @@ struct qmh_model {
 };
 
 /* the kernels of one decode step, by stage (which) and layer */
-enum { ST_QKV = 0, ST_WO = 1, ST_W13 = 2, ST_W2 = 3, ST_OUT = 4, ST_SCORES = 5, ST_PV = 6, ST_COUNT };
+enum { ST_QKV = 0, ST_WO = 1, ST_W13 = 2, ST_W2 = 3, ST_OUT = 4, ST_SCORES = 5, ST_PV = 6, ST_ATTN = 7, ST_COUNT };
 
 static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     const qmh_config *c = &m->cfg;
@@ -428,6 +437,10 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
                                       1.0f / sqrtf((float)m->hd), s);
     case ST_PV: /* src/model.c:147-154 */
         return qmh_launch_attn_pv(m->d_att, vl, m->d_xb, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_, s);
+    case ST_ATTN: /* src/model.c:137-156 in one launch */
+        if (!m->af_ok) return (int)hipErrorNotSupported;
+        return qmh_launch_attn_fused(m->d_q, kl, vl, m->d_xb, m->d_attp, pos_ptr, m->d_sync, c->n_heads, c->n_kv_heads,
+                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), l, c->n_layers, m->af_stall, s);
     case ST_WO: /* x += Wo xb (src/model.c:178-179) */
         mv_args_for(&L->wo, &a);
         a.x = m->d_xb;
@@ -476,23 +489,47 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     return (int)hipErrorInvalidValue;
 }
 
-static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax) {
+/* af: the attention in one launch (the step's position is below qmh_attn_fused_max_n()) */
+static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax, int af) {
     const qmh_config *c = &m->cfg;
-    LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, c->dim, c->vocab_size, m->d_tokpos, m->d_x, s));
+    LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, c->dim, c->vocab_size, m->d_tokpos, m->d_x, m->d_sync, s));
     static const int order[6] = {ST_QKV, ST_SCORES, ST_PV, ST_WO, ST_W13, ST_W2};
-    for (int l = 0; l < c->n_layers; l++)
-        for (int k = 0; k < 6; k++) LCHK(enqueue_stage(m, order[k], l, s));
+    static const int order_af[5] = {ST_QKV, ST_ATTN, ST_WO, ST_W13, ST_W2};
+    for (int l = 0; l < c->n_layers; l++) {
+        if (af)
+            for (int k = 0; k < 5; k++) LCHK(enqueue_stage(m, order_af[k], l, s));
+        else
+            for (int k = 0; k < 6; k++) LCHK(enqueue_stage(m, order[k], l, s));
+    }
     LCHK(enqueue_stage(m, ST_OUT, 0, s));
     if (with_argmax)
         LCHK(qmh_launch_argmax(m->d_logits, c->vocab_size, NULL, m->d_tokpos, m->d_record, c->max_seq, s));
     return 0;
 }
 
-/* one decode step on the library stream: a graph replay, or the same launches one by one */
-static hipError_t run_step(qmh_model *m, int with_argmax) {
-    if (m->use_graph) return hipGraphLaunch(with_argmax ? m->exec_greedy : m->exec_fwd, g_stream);
-    return enqueue_step(m, g_stream, with_argmax) ? hipErrorLaunchFailure : hipSuccess;
+/* one decode step at position pos on the library stream: a graph replay, or the same launches one by
+ * one */
+static hipError_t run_step(qmh_model *m, int with_argmax, int32_t pos) {
+    const int af = m->af_ok && pos < qmh_attn_fused_max_n();
+    if (m->use_graph)
+        return hipGraphLaunch(with_argmax ? (af ? m->exec_greedy_af : m->exec_greedy) : (af ? m->exec_fwd_af : m->exec_fwd),
+                              g_stream);
+    return enqueue_step(m, g_stream, with_argmax, af) ? hipErrorLaunchFailure : hipSuccess;
 }
+
+/* after a synchronization: the status of k_attn_fused's bounded waits since the last check (and the
+ * word cleared for the next). copied: the caller already copied d_sync[1] to h_sync before it
+ * synchronized */
+static int check_attn_sync_copied(qmh_model *m, int copied) {
+    if (!m->af_ok) return 0;
+    if (!copied) HIPCHK(hipMemcpy(m->h_sync, m->d_sync + 1, sizeof(uint32_t), hipMemcpyDeviceToHost));
+    if (*m->h_sync == 0) return 0;
+    const uint32_t st = *m->h_sync;
+    HIPCHK(hipMemset(m->d_sync + 1, 0, sizeof(uint32_t)));
+    return fail(st == 2 ? "attention: one-launch kernel given a context past its limit"
+                        : "attention: a workgroup's wait for its head's scores ran out");
+}
+static int check_attn_sync(qmh_model *m) { return check_attn_sync_copied(m, 0); }
 
 /* weight bytes one launch of a stage streams (the algorithmic bytes of the matvecs) */
 static double stage_weight_bytes(const qmh_model *m, int which) {
@@ -547,7 +584,7 @@ int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_st
     slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
     hipError_t e = hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream);
     if (e == hipSuccess) e = hipEventRecord(e0, g_stream);
-    for (int32_t k = 0; k < n_steps && e == hipSuccess; k++) e = run_step(m, 1);
+    for (int32_t k = 0; k < n_steps && e == hipSuccess; k++) e = run_step(m, 1, pos + k);
     if (e == hipSuccess) e = hipEventRecord(e1, g_stream);
     if (e == hipSuccess && out)
         e = hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream);
@@ -558,12 +595,12 @@ int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_st
     hipEventDestroy(e1);
     if (e != hipSuccess) return fail("time_greedy: %s", hipGetErrorString(e));
     if (ms) *ms = (double)t;
-    return 0;
+    return check_attn_sync(m);
 }
 
-static int capture(qmh_model *m, int with_argmax, hipGraph_t *g, hipGraphExec_t *ex) {
+static int capture(qmh_model *m, int with_argmax, int af, hipGraph_t *g, hipGraphExec_t *ex) {
     HIPCHK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(m, g_stream, with_argmax);
+    int rc = enqueue_step(m, g_stream, with_argmax, af);
     hipGraph_t graph = NULL;
     hipError_t e = hipStreamEndCapture(g_stream, &graph);
     if (rc) {
@@ -587,6 +624,10 @@ void qmh_model_free(qmh_model *m) {
     if (m->exec_greedy) hipGraphExecDestroy(m->exec_greedy);
     if (m->graph_fwd) hipGraphDestroy(m->graph_fwd);
     if (m->graph_greedy) hipGraphDestroy(m->graph_greedy);
+    if (m->exec_fwd_af) hipGraphExecDestroy(m->exec_fwd_af);
+    if (m->exec_greedy_af) hipGraphExecDestroy(m->exec_greedy_af);
+    if (m->graph_fwd_af) hipGraphDestroy(m->graph_fwd_af);
+    if (m->graph_greedy_af) hipGraphDestroy(m->graph_greedy_af);
     if (m->layers) {
         for (int l = 0; l < m->cfg.n_layers; l++) {
             weight_release(&m->layers[l].qkv);
@@ -600,10 +641,11 @@ void qmh_model_free(qmh_model *m) {
     void *dev[] = {m->d_embd,   m->d_norms,  m->d_rope,     m->d_x,    m->d_xb,   m->d_q,     m->d_hb,
                    m->d_hq,     m->d_att,    m->d_logits,   m->d_kt,   m->d_v,    m->d_tokpos, m->d_record,
                    m->d_pf_tok, m->d_pf_x,   m->d_pf_xb,    m->d_pf_q, m->d_pf_hb, m->d_pf_att, m->d_pf_logits,
-                   m->d_pf_xd,  m->d_pf_xc,  m->d_pf_xc2, m->d_pf_xd2};
+                   m->d_pf_xd,  m->d_pf_xc,  m->d_pf_xc2, m->d_pf_xd2, m->d_attp, m->d_sync};
     for (size_t i = 0; i < sizeof dev / sizeof dev[0]; i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_tokpos) hipHostFree(m->h_tokpos);
+    if (m->h_sync) hipHostFree(m->h_sync);
     if (m->h_logits) hipHostFree(m->h_logits);
     if (m->h_pf_tok) hipHostFree(m->h_pf_tok);
     free(m);
@@ -715,6 +757,17 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMemsetAsync(m->d_kt, 0, kv_bytes, g_stream));
     HIPCHK(hipMemsetAsync(m->d_v, 0, kv_bytes, g_stream));
     HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
+    /* the one-launch attention: its score words start at epoch 0, which no launch uses */
+    m->af_ok = getenv("QMH_NO_FUSED_ATTN") == NULL &&
+               qmh_attn_fused_supported(c->n_heads, c->n_kv_heads, m->hd, (int)S_);
+    m->af_stall = getenv("QMH_AF_FORCE_STALL") != NULL;
+    HIPCHK(hipMalloc((void **)&m->d_sync, sizeof(uint32_t) * 2));
+    HIPCHK(hipMemsetAsync(m->d_sync, 0, sizeof(uint32_t) * 2, g_stream));
+    HIPCHK(hipHostMalloc((void **)&m->h_sync, sizeof(uint32_t), hipHostMallocDefault));
+    if (m->af_ok) {
+        HIPCHK(hipMalloc((void **)&m->d_attp, sizeof(uint64_t) * (size_t)c->n_heads * S_));
+        HIPCHK(hipMemsetAsync(m->d_attp, 0, sizeof(uint64_t) * (size_t)c->n_heads * S_, g_stream));
+    }
     HIPCHK(hipHostMalloc((void **)&m->h_tokpos, sizeof(int32_t) * 4 * (size_t)S_, hipHostMallocDefault));
     HIPCHK(hipHostMalloc((void **)&m->h_logits, sizeof(float) * V, hipHostMallocDefault));
     /* batched prefill buffers (models whose matrices are all quantized) */
@@ -747,9 +800,12 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     }
     HIPCHK(hipStreamSynchronize(g_stream));
     m->use_graph = getenv("QMH_NO_GRAPH") == NULL;
-    if (m->use_graph && capture(m, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
-    if (m->use_graph && capture(m, 1, &m->graph_greedy, &m->exec_greedy)) return -1;
-    if (!m->use_graph && enqueue_step(m, g_stream, 0)) return -1; /* validate the launches once */
+    if (m->use_graph && capture(m, 0, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
+    if (m->use_graph && capture(m, 1, 0, &m->graph_greedy, &m->exec_greedy)) return -1;
+    if (m->use_graph && m->af_ok && capture(m, 0, 1, &m->graph_fwd_af, &m->exec_fwd_af)) return -1;
+    if (m->use_graph && m->af_ok && capture(m, 1, 1, &m->graph_greedy_af, &m->exec_greedy_af)) return -1;
+    if (!m->use_graph && enqueue_step(m, g_stream, 0, 0)) return -1; /* validate the launches once */
+    if (!m->use_graph && m->af_ok && enqueue_step(m, g_stream, 0, 1)) return -1;
     HIPCHK(hipStreamSynchronize(g_stream));
     return 0;
 }
@@ -848,15 +904,18 @@ float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
     m->h_tokpos[0] = token;
     m->h_tokpos[1] = pos;
     hipError_t e = hipMemcpyAsync(m->d_tokpos, m->h_tokpos, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream);
-    if (e == hipSuccess) e = run_step(m, 0);
+    if (e == hipSuccess) e = run_step(m, 0, pos);
     if (e == hipSuccess)
         e = hipMemcpyAsync(m->h_logits, m->d_logits, sizeof(float) * (size_t)m->cfg.vocab_size, hipMemcpyDeviceToHost,
                            g_stream);
+    if (e == hipSuccess && m->af_ok)
+        e = hipMemcpyAsync(m->h_sync, m->d_sync + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) {
         fail("forward: %s", hipGetErrorString(e));
         return NULL;
     }
+    if (check_attn_sync_copied(m, 1)) return NULL;
     return m->h_logits;
 }
 
@@ -1038,11 +1097,11 @@ int qmh_model_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t po
         slot[0] = tokens[i];
         slot[1] = pos0 + i;
         HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream));
-        HIPCHK(run_step(m, 0));
+        HIPCHK(run_step(m, 0, pos0 + i));
         if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * V, m->d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, g_stream));
     }
     HIPCHK(hipStreamSynchronize(g_stream));
-    return 0;
+    return check_attn_sync(m);
 }
 
 int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out) {
@@ -1052,11 +1111,11 @@ int qmh_model_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, 
     int32_t *slot = m->h_tokpos;
     slot[0] = token, slot[1] = pos, slot[2] = 0, slot[3] = 0;
     HIPCHK(hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 4, hipMemcpyHostToDevice, g_stream));
-    for (int32_t k = 0; k < n_steps; k++) HIPCHK(run_step(m, 1));
+    for (int32_t k = 0; k < n_steps; k++) HIPCHK(run_step(m, 1, pos + k));
     if (n_steps > 0 && out)
         HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
     HIPCHK(hipStreamSynchronize(g_stream));
-    return 0;
+    return check_attn_sync(m);
 }
 
 int qmh_model_time_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32_t pos0, int logits, double *ms) {
@@ -1078,7 +1137,7 @@ int qmh_model_time_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32
                 slot[0] = tokens[i];
                 slot[1] = pos0 + i;
                 e = hipMemcpyAsync(m->d_tokpos, slot, sizeof(int32_t) * 2, hipMemcpyHostToDevice, g_stream);
-                if (e == hipSuccess) e = run_step(m, 0);
+                if (e == hipSuccess) e = run_step(m, 0, pos0 + i);
             }
         }
     }
@@ -1091,7 +1150,7 @@ int qmh_model_time_prefill(qmh_model *m, const int32_t *tokens, int32_t n, int32
     if (rc) return -1;
     if (e != hipSuccess) return fail("time_prefill: %s", hipGetErrorString(e));
     if (ms) *ms = (double)t;
-    return 0;
+    return check_attn_sync(m);
 }
 
 int qmh_model_time_forward(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms) {
@@ -1445,13 +1504,13 @@ int qmh_model_sample(qmh_model *m, qmh_sampler *s, int32_t token, int32_t pos, i
     a.record = m->d_record;
     a.record_cap = m->cfg.max_seq;
     for (int32_t k = 0; k < n_steps; k++) {
-        HIPCHK(run_step(m, 0));
+        HIPCHK(run_step(m, 0, pos + k));
         LCHK(qmh_launch_sample(&a, g_stream));
     }
     if (n_steps > 0 && out)
         HIPCHK(hipMemcpyAsync(out, m->d_record, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, g_stream));
     HIPCHK(hipStreamSynchronize(g_stream));
-    return 0;
+    return check_attn_sync(m);
 }
 
 /* ------------------------------------------------------------------ generator */

@@ -17,6 +17,11 @@ passes. The formulas restate the kernels' own index arithmetic, line by line:
   * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:393-530: one workgroup per query head, float4 V
                           loads of its kv head clamped to position n-1 and column head_dim-4
   * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:532-555: kernel choice and dynamic LDS
+  * k_attn_fused<HD>      quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= 640): the
+                          K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
+                          score words, and that the slices of a head's workgroups cover its n
+                          positions exactly once (a position nobody writes would leave its readers
+                          waiting until their bounded wait runs out)
 This is a model: a kernel edit that changes an index must change it here too.
 """
 import numpy as np
@@ -207,6 +212,55 @@ def pv_mha_long(nh, nkv, hd, S, n, ext, lds_floats):
 
 LDS_MAX = 160 * 1024 - 1024  # per workgroup on gfx950, less the kernels' static LDS
 
+AF_TC = 640
+
+
+def af_lds_floats(hd):
+    ncg = hd // CW
+    spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
+    return max(spm * (hd + 4), AF_TC + CW * (AF_TC + 4))
+
+
+def fused(nh, nkv, hd, S, n, ext):
+    """k_attn_fused<HD> over grid (hd/16, nh) x 256 threads, n <= 640 positions."""
+    assert hd in (48, 64, 128) and S % 4 == 0 and S >= 4 and n <= min(AF_TC, S)
+    ncg, kvd = hd // CW, hd * nkv
+    spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
+    KS, KL4 = hd + 4, (spm // 4 * hd + WG - 1) // WG
+    assert spm <= WG
+    lds = af_lds_floats(hd)
+    assert 4 * lds <= LDS_MAX
+    tid = np.arange(WG)
+    inb("af q", np.arange(nh)[:, None] * hd + 4 * tid[tid < hd // 4][None, :] + 3, ext.q)
+    sp = ((n + ncg - 1) // ncg + 3) & ~3
+    covered = np.zeros(n, dtype=np.int64)
+    for cg in range(ncg):
+        p0 = cg * sp
+        npos = max(min(n - p0, sp), 0)
+        np4 = (npos + 3) >> 2
+        np4d = max(np4, 1)
+        assert 4 * np4 <= spm
+        e = (np.arange(KL4)[:, None] * WG + tid[None, :]).ravel()
+        d = np.minimum(e // np4d, hd - 1)
+        t = p0 + 4 * (e % np4d)
+        tc = np.minimum(t, S - 4)
+        for kvh in range(nkv):
+            for r in range(4):
+                inb("af K", kvh * hd * S + d * S + tc + r, ext.K)
+        on = e < np4 * hd
+        for j in range(4):
+            inb("af K LDS", (4 * (e[on] % np4d) + j) * KS + e[on] // np4d, lds)
+        ch = tid[tid < npos]
+        inb("af chain LDS", ch * KS + hd - 1, lds)
+        for h in range(nh):
+            inb("af score word", h * S + p0 + ch, ext.att)
+        covered[p0 + ch] += 1
+    assert (covered == 1).all(), "every position's score is written by exactly one workgroup"
+    SK = (AF_TC + WG - 1) // WG
+    t = tid[None, :] + WG * np.arange(SK)[:, None]
+    inb("af poll", np.arange(nh)[:, None] * S + t[t < n][None, :], ext.att)
+    pv_mha(AF_TC, nh, nkv, hd, S, n, ext, lds)
+
 
 def pv(nh, nkv, hd, S, pos, ext):
     """qmh_launch_attn_pv's choice of kernel and dynamic LDS bytes."""
@@ -237,6 +291,18 @@ def test_decode_attention_indices_in_bounds(shape):
     for pos in positions(S):
         scores(nh, nkv, hd, S, pos, ext)
         pv(nh, nkv, hd, S, pos, ext)
+        # the one-launch kernel: shapes qmh_attn_fused_supported takes, positions below 640
+        if hd in (48, 64, 128) and S % 4 == 0 and S >= 4 and pos + 1 <= AF_TC:
+            fused(nh, nkv, hd, S, pos + 1, ext)
+
+
+def test_fused_slices_cover_every_position():
+    """Every n in 1..640 and every head_dim the one-launch kernel takes: its workgroups' score slices
+    cover positions 0..n-1 once each (fused() asserts it), here with the other checks too."""
+    for hd in (48, 64, 128):
+        ext = Extents(2, 1, hd, 640)
+        for n in range(1, AF_TC + 1):
+            fused(2, 1, hd, 640, n, ext)
 
 
 def test_model_catches_an_out_of_range_clamp():
