@@ -555,6 +555,117 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
     pv_short<TC>(sv, vv, etv, s0, n, h, i0, hd, out, pv_smem);
 }
 
+// pv_short for the one-launch kernel: the same statistics, products and sums, with the products of
+// every position staged at once (Vs holds the whole context; this thread's exponentials read from
+// LDS together, then its 4*L4 products stored), one barrier, and the chain lanes (the first 16
+// threads) adding without further barriers, reading the next 32 positions' products while they add
+// the current ones. The chains stop at the last 32-position step holding a position below n (the
+// staged zeros past n change nothing: the sums start at +0 and are never -0).
+template <int TC>
+__device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1) / QMH_WG],
+                                              float4 (&vv)[TC * QMH_PV_CW / 4 / QMH_WG], uint64_t etv,
+                                              const float *x0p, int n, int h, int i0, int hd,
+                                              float *__restrict__ out, float *pv_smem) {
+    constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
+    constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
+    constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
+    constexpr int NW = QMH_WG / 64;
+    static_assert(TC % 32 == 0 && L4 * (QMH_WG / 4) == TC, "every position staged, whole 32-position steps");
+    float *P = pv_smem;       // [TC] exponentials e_t
+    float *Vs = pv_smem + TC; // [CW][VS] products, transposed
+    __shared__ float wmax[NW];
+    __shared__ double wsum[NW];
+    __shared__ double ser_s;
+    __shared__ uint64_t etab[32];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // softmax statistics (src/ops.c:100-112), as pv_short
+    if (tid < 32) etab[tid] = etv;
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < SK; k++)
+        if (tid + k * QMH_WG < n) m = sv[k] > m ? sv[k] : m;
+    m = qmh_wave_max(m);
+    if (lane == 0) wmax[wv] = m;
+    __syncthreads();
+    m = wmax[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = fmaxf(m, wmax[w]);
+    const float x0 = *x0p;
+    if (x0 != x0) m = x0;
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < SK; k++) {
+        const int t = tid + k * QMH_WG;
+        if (t < n) {
+            const float e = qmh_expf_t(sv[k] - m, etab);
+            P[t] = e;
+            sum += (double)e;
+        }
+    }
+    sum = qmh_wave_sum_d(sum);
+    if (lane == 0) wsum[wv] = sum;
+    __syncthreads();  // also publishes P
+    sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) sum += wsum[w];
+    const double d = qmh_sum_slack(sum, n);
+    float inv = qmh_recip_of_sum(sum - d);
+    if (inv != qmh_recip_of_sum(sum + d)) {  // uniform: the reference's serial order
+        if (tid == 0) {
+            double ser = 0.0;
+            for (int t = 0; t < n; t++) ser += (double)P[t];
+            ser_s = ser;
+        }
+        __syncthreads();
+        inv = qmh_recip_of_sum(ser_s);
+    }
+    // products p_t*v_t of every position, +0 past n
+    float pj[L4];
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int t = k * (QMH_WG / 4) + (tid >> 2);
+        pj[k] = t < n ? P[t] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < L4; k++) {
+        const int t = k * (QMH_WG / 4) + (tid >> 2);
+        const bool on = t < n;
+        const float p = pj[k] * inv;
+        const float4 v = vv[k];
+        float *dst = Vs + (size_t)(4 * (tid & 3)) * VS + t;
+        dst[0] = on ? p * v.x : 0.0f;
+        dst[VS] = on ? p * v.y : 0.0f;
+        dst[2 * VS] = on ? p * v.z : 0.0f;
+        dst[3 * VS] = on ? p * v.w : 0.0f;
+    }
+    __syncthreads();
+    if (tid < QMH_PV_CW) {
+        // out = out + p_t*v_t in t order, 32 positions per step
+        const float4 *v4 = (const float4 *)(Vs + (size_t)tid * VS);
+        const int nst = (n + 31) >> 5;
+        float acc = 0.0f;
+        float4 cur[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) cur[q] = v4[q];
+        for (int st = 0; st < nst; st++) {
+            float4 nxt[8];
+            const int sn = st + 1 < nst ? st + 1 : st;  // the last step re-reads itself
+#pragma unroll
+            for (int q = 0; q < 8; q++) nxt[q] = v4[8 * sn + q];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                acc = acc + cur[q].x;
+                acc = acc + cur[q].y;
+                acc = acc + cur[q].z;
+                acc = acc + cur[q].w;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q++) cur[q] = nxt[q];
+        }
+        if (i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
+    }
+}
+
 // ============================================================================ one launch per step
 
 // The decode step's whole attention in one launch, for contexts of up to QMH_AF_TC positions:
@@ -705,7 +816,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
     for (int k = 0; k < SK; k++) sv[k] = __uint_as_float((uint32_t)w[k]);
     if (tid == 0) x0s = sv[0];
     __syncthreads();  // the K slice is dead: its LDS is the V sum's from here
-    pv_short<TC>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
+    pv_short_flow<TC>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
 }
 
 // dynamic LDS bytes of k_attn_fused<HD>: the larger of the K slice and the V sum's buffers

@@ -101,11 +101,6 @@ __device__ __forceinline__ float qmh_expf_t(float x, const uint64_t *tab) {
 __device__ __forceinline__ float qmh_expf(float x) { return qmh_expf_t(x, qmh_exp2_tab); }
 // --------------------------------------------------------------------------- reductions
 
-__device__ __forceinline__ float qmh_wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
 template <int CTRL>
 __device__ __forceinline__ int qmh_dpp(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
@@ -119,6 +114,32 @@ __device__ __forceinline__ double qmh_dpp_d(double v) {
     const int lo = qmh_dpp<CTRL>(__double2loint(v)), hi = qmh_dpp<CTRL>(__double2hiint(v));
     return __hiloint2double(hi, lo);
 }
+// The value of lane ^ 16 and of lane ^ 32, VALU only (gfx950's v_permlane16_swap / v_permlane32_swap
+// with both operands v: lanes of the lower row/half get the upper's values in the second result,
+// lanes of the upper in the first), instead of an LDS round trip through ds_bpermute.
+__device__ __forceinline__ uint32_t qmh_xor16_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t qmh_xor32_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ double qmh_xor16_d(double v) {
+    return __hiloint2double((int)qmh_xor16_u((uint32_t)__double2hiint(v)), (int)qmh_xor16_u((uint32_t)__double2loint(v)));
+}
+__device__ __forceinline__ double qmh_xor32_d(double v) {
+    return __hiloint2double((int)qmh_xor32_u((uint32_t)__double2hiint(v)), (int)qmh_xor32_u((uint32_t)__double2loint(v)));
+}
+// max over the 64 lanes, every lane ending with it (DPP inside 16-lane rows, then the swaps)
+__device__ __forceinline__ float qmh_wave_max(float v) {
+    v = fmaxf(v, __int_as_float(qmh_dpp<QMH_DPP_QXOR1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(qmh_dpp<QMH_DPP_QXOR2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(qmh_dpp<QMH_DPP_HALF_MIRROR>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(qmh_dpp<QMH_DPP_MIRROR>(__float_as_int(v))));
+    v = fmaxf(v, __uint_as_float(qmh_xor16_u(__float_as_uint(v))));
+    return fmaxf(v, __uint_as_float(qmh_xor32_u(__float_as_uint(v))));
+}
 // sum over the 64 lanes (fixed order; all lanes get it): DPP within quads, 8- and 16-lane rows
 // (the half-mirror / mirror pair each lane with one in the other half), then lane ^ 16, ^ 32
 __device__ __forceinline__ double qmh_wave_sum_d(double v) {
@@ -126,8 +147,8 @@ __device__ __forceinline__ double qmh_wave_sum_d(double v) {
     v += qmh_dpp_d<QMH_DPP_QXOR2>(v);
     v += qmh_dpp_d<QMH_DPP_HALF_MIRROR>(v);
     v += qmh_dpp_d<QMH_DPP_MIRROR>(v);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
+    v += qmh_xor16_d(v);
+    v += qmh_xor32_d(v);
     return v;
 }
 

@@ -222,12 +222,16 @@ def af_lds_floats(hd):
 
 
 def fused(nh, nkv, hd, S, n, ext):
-    """k_attn_fused<HD> over grid (hd/16, nh) x 256 threads, n <= 640 positions."""
+    """k_attn_fused<HD> over grid (hd/16, nh) x 256 threads, n <= 640 positions: every thread loads its
+    part of the K slice and its V float4s (as k_attn_pv_mha), the threads below the slice's position
+    count run the score chains, every thread reads the head's scores, stages its products for all 640
+    positions, and the first 16 threads run the V sum's chains (pv_short_flow)."""
     assert hd in (48, 64, 128) and S % 4 == 0 and S >= 4 and n <= min(AF_TC, S)
     ncg, kvd = hd // CW, hd * nkv
     spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
     KS, KL4 = hd + 4, (spm // 4 * hd + WG - 1) // WG
-    assert spm <= WG
+    L4, SK, VS = AF_TC * CW // 4 // WG, (AF_TC + WG - 1) // WG, AF_TC + 4
+    assert spm <= WG and L4 * (WG // 4) == AF_TC
     lds = af_lds_floats(hd)
     assert 4 * lds <= LDS_MAX
     tid = np.arange(WG)
@@ -250,16 +254,33 @@ def fused(nh, nkv, hd, S, n, ext):
         on = e < np4 * hd
         for j in range(4):
             inb("af K LDS", (4 * (e[on] % np4d) + j) * KS + e[on] // np4d, lds)
-        ch = tid[tid < npos]
-        inb("af chain LDS", ch * KS + hd - 1, lds)
+        rows = tid[tid < npos]
+        inb("af chain LDS", rows * KS + hd - 1, lds)
         for h in range(nh):
-            inb("af score word", h * S + p0 + ch, ext.att)
-        covered[p0 + ch] += 1
+            inb("af score word", h * S + p0 + rows, ext.att)
+        covered[p0 + rows] += 1
+        # V: position k*64 + tid/4 clamped to n-1, columns i0 + 4*(tid%4) clamped to hd-4
+        c = cg * CW + 4 * (tid & 3)
+        cc = np.where(c <= hd - 4, c, hd - 4)
+        tv = np.minimum(np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :], n - 1)
+        for kvh in range(nkv):
+            for r in range(4):
+                inb("af V", tv * kvd + kvh * hd + cc[None, :] + r, ext.V)
     assert (covered == 1).all(), "every position's score is written by exactly one workgroup"
-    SK = (AF_TC + WG - 1) // WG
     t = tid[None, :] + WG * np.arange(SK)[:, None]
     inb("af poll", np.arange(nh)[:, None] * S + t[t < n][None, :], ext.att)
-    pv_mha(AF_TC, nh, nkv, hd, S, n, ext, lds)
+    inb("af P", t[t < n], AF_TC)
+    # staging: every thread, positions k*64 + tid/4 (all < 640), rows 4*(tid%4) + r of Vs
+    ts = np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :]
+    assert ts.max() < AF_TC
+    inb("af P read", ts[ts < n], AF_TC)
+    for r in range(4):
+        inb("af stage", AF_TC + (4 * (tid & 3) + r)[None, :] * VS + ts, lds)
+    # chains: 16 lanes, 32-position steps up to the last holding a position below n
+    nst = (n + 31) >> 5
+    inb("af chain", AF_TC + np.arange(CW)[:, None] * VS + 4 * (8 * (nst - 1) + np.arange(8))[None, :] + 3, lds)
+    assert 32 * nst <= AF_TC
+    mha_out(nh, hd, ext)
 
 
 def pv(nh, nkv, hd, S, pos, ext):
