@@ -113,9 +113,12 @@ def host_cpus():
             "sockets": len({p for p, _ in cores}) or None, "affinity": len(os.sched_getaffinity(0))}
 
 
-def cpu_baseline(path, w, q, P, G):
-    """The compiled reference (oracle/_ref/ref_driver) on a bounded sample of the workload: the median of
-    three runs on the box's CPU share of threads, and one single-thread run."""
+def cpu_baseline(path, w, q, P, G, runs=3, warm=True, one_thread=True):
+    """The compiled reference (oracle/_ref/ref_driver, best CPU ISA) on the config's whole workload, as
+    BASELINE.md's plan has it: P sequential qm_model_forward calls over the prompt (the reference's
+    only prompt method, src/main.c:127-130), then G greedy steps (bench/bench.c:143-149), max_seq
+    P + G, on the box's CPU share of threads; the median of `runs` runs after one untimed warm pass
+    over the mmap'd file; optionally one single-thread run on a short sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _bind import REF_DRIVER, ref_run
 
@@ -125,30 +128,33 @@ def cpu_baseline(path, w, q, P, G):
     isa = "avx512" if (" avx512f " in flags and " avx512bw " in flags and " avx512vl " in flags) else "avx2"
     host = host_cpus()
     threads = min(host["affinity"], CPU_SHARE)
-    Ps, Gs = min(P, 64), min(G, 32)
-    prompt = q.prompt_ids(Ps, w.vocab_size)
-    runs = []
-    for r in range(3):
-        res, _ = ref_run(path, prompt, Gs, isa=isa, threads=threads, max_seq=Ps + Gs, logits=False, warm=r == 0,
-                         timeout=900)
-        runs.append(res)
-        log(f"[bench] cpu baseline run {r}: decode {res['decode_tok_s']:.2f} prefill {res['prompt_tok_s']:.2f} tok/s")
-    P1, G1 = min(P, 8), min(G, 8)
-    one, _ = ref_run(path, prompt[:P1], G1, isa=isa, threads=1, max_seq=P1 + G1, logits=False, timeout=900)
-    log(f"[bench] cpu baseline 1 thread: decode {one['decode_tok_s']:.2f} prefill {one['prompt_tok_s']:.2f} tok/s")
-    dec = [r["decode_tok_s"] for r in runs]
-    pre = [r["prompt_tok_s"] for r in runs]
-    return {
+    prompt = q.prompt_ids(P, w.vocab_size)
+    res = []
+    for r in range(runs):
+        out, _ = ref_run(path, prompt, G, isa=isa, threads=threads, max_seq=P + G, logits=False,
+                         warm=warm and r == 0, timeout=900)
+        res.append(out)
+        log(f"[bench] cpu baseline {w.name} run {r}: decode {out['decode_tok_s']:.2f} prefill "
+            f"{out['prompt_tok_s']:.2f} tok/s")
+    dec = [x["decode_tok_s"] for x in res]
+    pre = [x["prompt_tok_s"] for x in res]
+    cb = {
         "value": round(statistics.median(dec), 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-        "isa": runs[0]["isa"], "prefill_tok_s": round(statistics.median(pre), 3),
+        "isa": res[0]["isa"], "prefill_tok_s": round(statistics.median(pre), 3),
         "runs_decode_tok_s": [round(x, 3) for x in dec], "runs_prefill_tok_s": [round(x, 3) for x in pre],
-        "one_thread": {"decode_tok_s": round(one["decode_tok_s"], 3), "prefill_tok_s": round(one["prompt_tok_s"], 3),
-                       "sample": f"{P1} prompt + {G1} decode tokens"},
         "host": host,
-        "sample": f"same {w.name} .qlm file; {Ps} prompt tokens (sequential qm_model_forward, logits at every "
-                  f"position) + {Gs} greedy decode steps, max_seq {Ps + Gs}, QUILLM isa {runs[0]['isa']}, {threads} "
-                  f"threads (the box's CPU share for one GPU), median of 3 runs after one untimed warm pass",
+        "sample": f"the whole {w.name} workload on the same .qlm file: {P} prompt tokens (sequential "
+                  f"qm_model_forward, logits at every position) + {G} greedy decode steps, max_seq {P + G}, "
+                  f"QUILLM isa {res[0]['isa']}, {threads} threads (the box's CPU share for one GPU), median "
+                  f"of {runs} run{'s' if runs > 1 else ''}" + (" after one untimed warm pass" if warm else ""),
     }
+    if one_thread:
+        P1, G1 = min(P, 8), min(G, 8)
+        one, _ = ref_run(path, prompt[:P1], G1, isa=isa, threads=1, max_seq=P1 + G1, logits=False, timeout=900)
+        log(f"[bench] cpu baseline 1 thread: decode {one['decode_tok_s']:.2f} prefill {one['prompt_tok_s']:.2f} tok/s")
+        cb["one_thread"] = {"decode_tok_s": round(one["decode_tok_s"], 3), "prefill_tok_s": round(one["prompt_tok_s"], 3),
+                            "sample": f"{P1} prompt + {G1} decode tokens"}
+    return cb
 
 
 def model_path(w, tag):
@@ -200,15 +206,19 @@ def measure(q, w, P, K, W, detail=False):
         if detail:
             flops = prefill_flops(w, P, P)
             ach = flops / (pf_all * 1e-3)
+            valu_ms = prefill_valu_floor_s(w, P, P) * 1e3
             out["prefill_roofline"] = {
                 "bound": "mfma", "unit": "TOP/s", "achieved": round(ach / 1e12, 2), "peak": INT8_PEAK_TOPS,
                 "frac": round(ach / 1e12 / INT8_PEAK_TOPS, 4), "flops": int(flops),
-                "frac_of_fp32_mfma": round(ach / 1e12 / FP32_MFMA_PEAK_TFS, 4),
-                "valu_floor_ms": round(prefill_valu_floor_s(w, P, P) * 1e3, 3),
+                "valu_floor_ms": round(valu_ms, 3), "frac_of_valu_floor": round(valu_ms / pf_all, 4),
                 "note": "int8 MFMA block dots and f16 MFMA scale products (both exact) + the bitwise f32 epilogue "
-                        "on the VALU (3 ops per row, token, block); flops counted as the reference's P forwards, "
-                        "every position's logits included",
+                        "on the VALU (3 ops per row, token, block), whose floor bounds this path more tightly than "
+                        "the int8 peak; flops counted as the reference's P forwards, every position's logits "
+                        "included",
             }
+            # the same flops over the FP32-MFMA peak the north star names (above 1: the exact integer
+            # dots run on int8 MFMA, so this is a comparison, not a roofline fraction)
+            out["prefill_vs_fp32_mfma_peak"] = round(ach / 1e12 / FP32_MFMA_PEAK_TFS, 4)
             # the same steps sampled on the device with the reference CLI's default sampler
             # (src/main.c:70-72: temperature 0.8, top-k 0, top-p 0.95, seed 42); wall clock, synchronous
             with q.Sampler(w.vocab_size, 0.8, 0, 0.95, 42) as smp:
@@ -226,8 +236,13 @@ def measure(q, w, P, K, W, detail=False):
                                 "ms_per_step": round(b_ms / K, 3)})
             out["batched_decode"] = batched
             stages = {}
-            for st in ("qkv", "wo", "w13", "w2", "output", "attn_scores", "attn_pv"):
-                ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=P + K - 1)
+            for st in ("qkv", "wo", "w13", "w2", "output", "attn", "attn_scores", "attn_pv"):
+                if st == "attn" and P + K - 1 >= 640:
+                    continue  # the one-launch attention takes positions below 640
+                try:
+                    ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=P + K - 1)
+                except q.QmhError:
+                    continue  # a head shape the one-launch attention does not take
                 stages[st] = {"us_per_launch": round(ms * 1e3, 3),
                               "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1) if nbytes else None,
                               "weight_MB": round(nbytes / 1e6, 3)}
@@ -241,6 +256,7 @@ def measure(q, w, P, K, W, detail=False):
                 "traffic": pmc_traffic(f"k_matvec_w13_{w.wtype}_{w.name}_pmc.txt"),
                 "bytes_per_launch": int(bytes_w13), "us_per_launch": round(ms_w13 * 1e3, 3)}
             out["setup_s"] = {"generate": round(gen_s, 1), "load": round(load_s, 1)}
+            out["kernel_rows"] = kernel_rows(q)
         m.close()
     except BaseException:
         if os.path.exists(path):
@@ -293,6 +309,73 @@ def probe_stream(q, w, grids=(256, 512, 1024), reps=20):
                              "bytes": int(sum(arr)), "us_per_layer": round(us[0], 2),
                              "GBps": round(sum(arr) / (us[0] * 1e-6) / 1e9, 1)}
     del pool
+    return out
+
+
+def kernel_rows(q, n=4096, gemm_n=512):
+    """The reference bench's kernel rows (bench/bench.c:63-123; README.md:163-173) on the device:
+    qmh_matvec at n x n for q8_0, q4_0 and f32 weights, and qmh_matmul_nt at gemm_n^3. Device time per
+    call from HIP events over back-to-back calls. 'hbm': calls cycle through copies of the matrix
+    whose total exceeds the 256 MB Infinity Cache, so the weights come from HBM; 'cached': one matrix
+    over and over (the reference bench's own loop). GFLOP/s counts 2*rows*cols per matvec as the
+    reference does (README.md:161)."""
+    import ctypes
+
+    import numpy as np
+
+    L = q.load_library()
+    rs = np.random.default_rng(5)
+    x = q.DeviceBuffer.from_array(rs.standard_normal(n).astype(np.float32))
+    y = q.DeviceBuffer(4 * n)
+    out = {}
+    for name, dtype, bb in (("q8_0", 2, 34), ("q4_0", 3, 18), ("f32", 0, None)):
+        if bb is None:
+            host = rs.standard_normal((n, n)).astype(np.float32) * 0.02
+            row_b = 4 * n
+        else:
+            nb = (n + 31) // 32
+            blocks = rs.integers(0, 256, (n, nb, bb), dtype=np.uint8)
+            scale = np.float16(0.01).view(np.uint16)
+            blocks[:, :, 0], blocks[:, :, 1] = scale & 0xff, scale >> 8
+            host = blocks.reshape(n, nb * bb)
+            row_b = nb * bb
+        mbytes = n * row_b
+        copies = max(1, -(-300_000_000 // mbytes))  # past the Infinity Cache
+        ws = []
+        try:
+            for _ in range(copies):
+                h = L.qmh_weight_upload(dtype, n, n, np.ascontiguousarray(host).ctypes.data)
+                if not h:
+                    raise q.QmhError(f"qmh_weight_upload: {q.last_error()}")
+                ws.append(h)
+            row = {"bytes": mbytes}
+            for tag, nw in (("hbm", copies), ("cached", 1)):
+                arr = (ctypes.c_void_p * nw)(*ws[:nw])
+                ms = ctypes.c_double()
+                iters = max(3 * copies, 24)
+                q._check(L.qmh_time_matvec(arr, nw, x.ptr, y.ptr, iters, ctypes.byref(ms)), "time_matvec")  # warm
+                q._check(L.qmh_time_matvec(arr, nw, x.ptr, y.ptr, iters, ctypes.byref(ms)), "time_matvec")
+                us = ms.value * 1e3
+                row[tag] = {"us_per_call": round(us, 3), "GBps": round(mbytes / (us * 1e-6) / 1e9, 1),
+                            "frac_of_hbm_peak": round(mbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                            "GFLOPs": round(2.0 * n * n / (us * 1e-6) / 1e9, 1)}
+            out[f"matvec_{name}_{n}x{n}"] = row
+        finally:
+            for h in ws:
+                L.qmh_weight_free(h)
+    M = gemm_n
+    A = q.DeviceBuffer.from_array(rs.standard_normal((M, M)).astype(np.float32))
+    B = q.DeviceBuffer.from_array(rs.standard_normal((M, M)).astype(np.float32))
+    C = q.DeviceBuffer(4 * M * M)
+    ms = ctypes.c_double()
+    q._check(L.qmh_time_matmul_nt(A.ptr, B.ptr, C.ptr, M, M, M, 5, ctypes.byref(ms)), "time_matmul_nt")
+    q._check(L.qmh_time_matmul_nt(A.ptr, B.ptr, C.ptr, M, M, M, 20, ctypes.byref(ms)), "time_matmul_nt")
+    flops = 2.0 * M * M * M
+    out[f"matmul_nt_f32_{M}^3"] = {
+        "us_per_call": round(ms.value * 1e3, 3), "GFLOPs": round(flops / (ms.value * 1e-3) / 1e9, 1),
+        "frac_of_valu_floor": round(flops / (ms.value * 1e-3) / VALU_LANE_OPS, 4),
+        "note": "the scalar ISA's rounding order (K panels of 256, one serial sum per output per panel): a "
+                "multiply and an add per term on the fp32 VALU, so the floor is 2*M*N*K lane operations"}
     return out
 
 
@@ -381,7 +464,8 @@ def main():
     }
     for k in ("prefill_tok_s", "prefill_last_logits_tok_s", "prefill_ms", "prefill_roofline", "forward_tok_s",
               "sampled_decode_tok_s", "batched_decode", "decode_bytes_per_token", "decode_hbm_frac",
-              "decode_roofline_tok_s", "roofline", "stages", "greedy_ids_head", "setup_s"):
+              "decode_roofline_tok_s", "roofline", "stages", "kernel_rows", "prefill_vs_fp32_mfma_peak",
+              "greedy_ids_head", "setup_s"):
         out[k] = head[k]
     out["timing"] = ("decode: HIP events around K graph replays (device argmax, no host round trip); forward_tok_s: "
                      "host clock around K qmh_model_forward calls with the logits copied to the host and a host "
@@ -390,8 +474,8 @@ def main():
                      "reference's prompt loop) or only the last one's")
     try:
         if not args.no_cpu:
-            log(f"[bench] cpu baseline: reference on a sample of {w.name}")
-            cb = cpu_baseline(path, w, q, P, head["decode_steps"])
+            log(f"[bench] cpu baseline: reference on {w.name}")
+            cb = cpu_baseline(path, w, q, P, w.n_gen)
             if cb is not None:
                 out["cpu_baseline"] = cb
     finally:
@@ -403,7 +487,16 @@ def main():
                 continue
             wc = q.WORKLOADS[name]
             r, p = measure(q, wc, wc.n_prompt, wc.n_gen, W)
-            os.remove(p)
+            try:
+                if not args.no_cpu:
+                    # the reference on the config's whole workload, one run (the file is in /dev/shm)
+                    cb = cpu_baseline(p, wc, q, wc.n_prompt, wc.n_gen, runs=1, warm=False, one_thread=False)
+                    if cb is not None:
+                        r["cpu_reference"] = {"decode_tok_s": cb["value"], "prefill_tok_s": cb["prefill_tok_s"],
+                                              "threads": cb["cores"], "isa": cb["isa"],
+                                              "sample": f"{wc.n_prompt} prompt + {wc.n_gen} greedy, one run"}
+            finally:
+                os.remove(p)
             others[name] = {k: v for k, v in r.items() if k != "workload"}
         out["configs"] = others
     print(json.dumps(out), flush=True)

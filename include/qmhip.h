@@ -191,8 +191,8 @@ int qmh_sampler_diag(const qmh_sampler *s, double diag[8], float *probs);
 
 /* qmh_sample without a sampler object, allocating nothing: no counterpart in the reference. It is
  * for callers that cannot allocate device memory (code under HIP graph capture, serving loops).
- * Same draw as qm_sample (src/sampler.c:50-106) with a sampler of these parameters, normalised as
- * qm_sampler_init does; *rng (device memory) holds the xorshift64* state and is advanced in place,
+ * The same draw as qmh_sample with a sampler created by qmh_sampler_create from these parameters;
+ * *rng (device memory) holds the xorshift64* state and is advanced in place,
  * *out (device) receives the token, asynchronously on the stream (NULL = the library's). Scratch:
  * one static device array of 3186944 bytes per GPU, held until the process ends, so n_vocab is at
  * most 131072 (-1 otherwise). Calls that overlap on one GPU race on that array. qmh_init must have
@@ -220,6 +220,13 @@ int qmh_model_sample(qmh_model *m, qmh_sampler *s, int32_t token, int32_t pos, i
  * attention). Overwrites the KV cache entries at pos. */
 int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double *ms_per_launch,
                          double *bytes_per_launch);
+/* The reference bench's kernel rows (bench/bench.c:63-123, which time qm_matvec and qm_matmul_nt with
+ * a host clock) on the device: the average device time (HIP events on the library stream) of `iters`
+ * back-to-back qmh_matvec calls, call i on W[i % nw] (weights of one dtype and shape: several
+ * copies make the reads come from HBM rather than a cache), and of qmh_matmul_nt calls. 0 or -1. */
+int qmh_time_matvec(const qmh_weight *const *W, int nw, const float *x, float *y, int iters, double *ms_per_call);
+int qmh_time_matmul_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K, int iters,
+                       double *ms_per_call);
 /* qmh_model_greedy, with HIP events around the n_steps graph replays (*ms = their total). */
 int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms);
 /* qmh_model_prefill of n tokens at pos0, with HIP events around it (*ms). logits: 0 none, 1 the last

@@ -75,6 +75,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmh_weight_upload": (vp, [ctypes.c_int, i64, i64, vp]),
         "qmh_weight_free": (None, [vp]),
         "qmh_matvec": (ctypes.c_int, [vp, vp, vp, vp, vp]),
+        "qmh_time_matvec": (ctypes.c_int, [ctypes.POINTER(vp), ctypes.c_int, vp, vp, ctypes.c_int,
+                                           ctypes.POINTER(ctypes.c_double)]),
+        "qmh_time_matmul_nt": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
         "qmh_rmsnorm_matvec": (ctypes.c_int, [vp, vp, vp, f32, vp, vp, vp]),
         "qmh_matmul_nt": (ctypes.c_int, [vp, vp, vp, i64, i64, i64, vp]),
         "qmh_rmsnorm": (ctypes.c_int, [vp, vp, vp, i64, f32, vp]),

@@ -624,42 +624,118 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     }
 }
 
-// f32 weights (src/kernels_scalar.c:6-10 via src/ops.c:42-45): lane per row, x in LDS,
-// s = +0; s = s + w_i*x_i in index order.
+// f32 weights (src/kernels_scalar.c:6-10 via src/ops.c:42-45): s = +0; s = s + w_i*x_i in index
+// order, one lane per row. A workgroup owns MF_R consecutive rows. Their weights stream through LDS
+// in chunks of MF_C columns, coalesced (64 consecutive threads read 1 KB of one row). The activation (RMSNorm'd when a gain is given, as the reference's
+// (x*inv)*w) sits in LDS for every chunk. Up to three chunks are ahead of the chains: one in LDS,
+// two in registers.
+#define MF_R 16
+#define MF_C 256
+#define MF_L4 (MF_R * MF_C / 4 / QMH_WG)  // float4 loads per thread per chunk
 __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
+    static_assert(MF_L4 * QMH_WG * 4 == MF_R * MF_C && MF_C % 4 == 0, "whole float4 chunks");
+    constexpr int TS = MF_C + 4;  // LDS row stride of a chunk (== 4 mod 64 floats)
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
-    float *xs = (float *)smem;
-    const int n = a.cols;
+    float *xs = (float *)smem;                                    // [cols rounded up to MF_C]
+    const int n = a.cols, nch = (n + MF_C - 1) / MF_C, tid = threadIdx.x;
+    float *tile = xs + (size_t)nch * MF_C;                        // [2][MF_R][TS]
+    const int r0 = blockIdx.x * MF_R;
+    // chunk c's loads: float4 f = k*QMH_WG + tid is row f / (MF_C/4), columns 4*(f % (MF_C/4)) ..; rows
+    // past the matrix re-read its last row, columns past n read the row's last whole float4 (or,
+    // for n % 4 != 0, element by element; the chain stops at n either way)
+    const float *W = (const float *)a.codes;
+    float4 ld[2][MF_L4];
+    auto issue = [&](int c, float4(&d)[MF_L4]) {
+#pragma unroll
+        for (int k = 0; k < MF_L4; k++) {
+            const int f = k * QMH_WG + tid, rr = f / (MF_C / 4), col = c * MF_C + 4 * (f % (MF_C / 4));
+            const int row = r0 + rr < a.rows ? r0 + rr : a.rows - 1;
+            const float *wr = W + (size_t)row * n;
+            if ((n & 3) == 0) {
+                d[k] = qmh_ld_nt4(wr + (col <= n - 4 ? col : n - 4));
+            } else {
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = wr[col + j < n ? col + j : n - 1];
+                d[k] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    };
+    auto stash = [&](const float4(&d)[MF_L4], float *t) {
+#pragma unroll
+        for (int k = 0; k < MF_L4; k++) {
+            const int f = k * QMH_WG + tid;
+            *(float4 *)(t + (f / (MF_C / 4)) * TS + 4 * (f % (MF_C / 4))) = d[k];
+        }
+    };
+    issue(0, ld[0]);
+    if (nch > 1) issue(1, ld[1]);
+    // the activation, normalised as the reference does when a gain is given (src/ops.c:93-98)
     float inv = 1.0f;
     if (a.norm_w) {
         double ss = 0.0;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            double v = (double)a.x[i];
+        for (int i = tid; i < n; i += QMH_WG) {
+            const double v = (double)a.x[i];
             ss += v * v;
         }
         ss = qmh_block_sum_d(ss, red);
         const double d = qmh_sum_slack(ss, n);
         inv = qmh_rms_inv(ss - d, n, a.eps);
         if (inv != qmh_rms_inv(ss + d, n, a.eps)) {  // uniform; serial sum as the reference
-            if (threadIdx.x == 0) {
-                double s = 0.0;
-                for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];
-                red[8] = s;
+            if (tid == 0) {
+                double sr = 0.0;
+                for (int i = 0; i < n; i++) sr += (double)a.x[i] * (double)a.x[i];
+                red[8] = sr;
             }
             __syncthreads();
             inv = qmh_rms_inv(red[8], n, a.eps);
         }
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = a.norm_w ? a.x[i] * inv * a.norm_w[i] : a.x[i];
+    for (int i = tid; i < nch * MF_C; i += QMH_WG)
+        xs[i] = i < n ? (a.norm_w ? a.x[i] * inv * a.norm_w[i] : a.x[i]) : 0.0f;
+    stash(ld[0], tile);
+    if (nch > 2) issue(2, ld[0]);
     __syncthreads();
-    const int row = blockIdx.x * blockDim.x + threadIdx.x;
-    const float *w = (const float *)a.codes + (size_t)(row < a.rows ? row : 0) * n;
     float s = 0.0f;
-    for (int i = 0; i < n; i++) s = s + w[i] * xs[i];
+    // chunk k is loaded into registers ld[k % 2]. Step c: the chains add chunk c from LDS buffer
+    // c % 2, chunk c+1 (registers nxt) goes to LDS buffer (c+1) % 2 once it lands (the waves without
+    // chain lanes do so while the chains add), then those registers take chunk c+3 (unrolled by two:
+    // the register buffers are indexed statically)
+    auto step = [&](int c, float4(&nxt)[MF_L4]) {
+        const int b = c & 1;
+        if (tid < MF_R) {
+            const float4 *wr = (const float4 *)(tile + (size_t)b * MF_R * TS + tid * TS);
+            const float4 *xr = (const float4 *)(xs + (size_t)c * MF_C);
+            const int m = n - c * MF_C < MF_C ? n - c * MF_C : MF_C;
+            if (m == MF_C) {
+#pragma unroll 8
+                for (int j = 0; j < MF_C / 4; j++) {
+                    const float4 w4 = wr[j], x4 = xr[j];
+                    s = s + w4.x * x4.x;
+                    s = s + w4.y * x4.y;
+                    s = s + w4.z * x4.z;
+                    s = s + w4.w * x4.w;
+                }
+            } else {
+                const float *w1 = (const float *)wr, *x1 = (const float *)xr;
+                for (int j = 0; j < m; j++) s = s + w1[j] * x1[j];
+            }
+        }
+        if (c + 1 < nch) {
+            stash(nxt, tile + (size_t)(b ^ 1) * MF_R * TS);
+            if (c + 3 < nch) issue(c + 3, nxt);
+        }
+        __syncthreads();
+    };
+    for (int c = 0; c < nch; c += 2) {
+        step(c, ld[1]);
+        if (c + 1 < nch) step(c + 1, ld[0]);
+    }
+    const int row = r0 + (tid & (MF_R - 1));
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
     const EpiIn e = epi_fetch(a, row, pos);
-    mv_epilogue(a, row, s, threadIdx.x & 15, QMH_TILE_R, pos, e, qmh_exp2_tab);
+    if (tid < 64) mv_epilogue(a, tid < MF_R ? row : a.rows, s, tid & (MF_R - 1), MF_R, pos, e, qmh_exp2_tab);
 }
 
 extern "C" int qmh_matvec_max_cols(int norm) {
@@ -702,8 +778,14 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     return (int)hipGetLastError();
 }
 
+// dynamic LDS of k_matvec_f32: the activation rounded up to whole chunks, then two chunks
+static size_t mf_lds_bytes(int cols) {
+    return sizeof(float) * ((size_t)(cols + MF_C - 1) / MF_C * MF_C + 2 * (size_t)MF_R * (MF_C + 4));
+}
+
 extern "C" int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream) {
-    const int grid = (a->rows + QMH_WG - 1) / QMH_WG;
-    hipLaunchKernelGGL(k_matvec_f32, dim3(grid), dim3(QMH_WG), (size_t)a->cols * 4, (hipStream_t)stream, *a);
+    if (a->rows < 1 || a->cols < 1 || mf_lds_bytes(a->cols) > 160 * 1024 - 1024) return (int)hipErrorInvalidValue;
+    const int grid = (a->rows + MF_R - 1) / MF_R;
+    hipLaunchKernelGGL(k_matvec_f32, dim3(grid), dim3(QMH_WG), mf_lds_bytes(a->cols), (hipStream_t)stream, *a);
     return (int)hipGetLastError();
 }

@@ -573,6 +573,71 @@ int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double
     return 0;
 }
 
+/* HIP events around `iters` calls of body(i) on the library stream: ms per call */
+static int time_calls(int iters, int (*body)(void *, int), void *ctx, double *ms_per_call, const char *what) {
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    int rc = 0;
+    hipError_t e = hipEventRecord(e0, g_stream);
+    for (int i = 0; i < iters && e == hipSuccess && rc == 0; i++) rc = body(ctx, i);
+    if (e == hipSuccess && rc == 0) e = hipEventRecord(e1, g_stream);
+    if (e == hipSuccess && rc == 0) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess && rc == 0) e = hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc) return fail("%s launch: %s", what, hipGetErrorString((hipError_t)rc));
+    if (e != hipSuccess) return fail("%s: %s", what, hipGetErrorString(e));
+    if (ms_per_call) *ms_per_call = (double)ms / iters;
+    return 0;
+}
+
+struct mv_time_ctx {
+    const qmh_weight *const *w;
+    int nw;
+    const float *x;
+    float *y;
+};
+static int mv_time_body(void *p, int i) {
+    const struct mv_time_ctx *c = p;
+    qmh_mv_args a;
+    mv_args_for(c->w[i % c->nw], &a);
+    a.x = c->x;
+    a.epi = QMH_EPI_STORE;
+    a.out0 = c->y;
+    return mv_launch(&a, g_stream);
+}
+
+int qmh_time_matvec(const qmh_weight *const *W, int nw, const float *x, float *y, int iters, double *ms_per_call) {
+    if (ensure()) return -1;
+    if (!W || nw < 1 || !x || !y || iters < 1) return fail("time_matvec: bad arguments");
+    for (int i = 0; i < nw; i++)
+        if (!W[i] || W[i]->dtype != W[0]->dtype || W[i]->rows != W[0]->rows || W[i]->cols != W[0]->cols)
+            return fail("time_matvec: the weights must share dtype and shape");
+    struct mv_time_ctx c = {W, nw, x, y};
+    return time_calls(iters, mv_time_body, &c, ms_per_call, "time_matvec");
+}
+
+struct mm_time_ctx {
+    const float *A, *B;
+    float *C;
+    int64_t M, N, K;
+};
+static int mm_time_body(void *p, int i) {
+    (void)i;
+    const struct mm_time_ctx *c = p;
+    return qmh_launch_gemm_nt(c->A, c->B, c->C, c->M, c->N, c->K, g_stream);
+}
+
+int qmh_time_matmul_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K, int iters,
+                       double *ms_per_call) {
+    if (ensure()) return -1;
+    if (!A || !B || !C || M < 1 || N < 1 || K < 1 || iters < 1) return fail("time_matmul_nt: bad arguments");
+    struct mm_time_ctx c = {A, B, C, M, N, K};
+    return time_calls(iters, mm_time_body, &c, ms_per_call, "time_matmul_nt");
+}
+
 int qmh_model_time_greedy(qmh_model *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out, double *ms) {
     if (!m || n_steps < 1 || token < 0 || token >= m->cfg.vocab_size || pos < 0 ||
         (int64_t)pos + n_steps > m->cfg.max_seq)
@@ -795,8 +860,12 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         HIPCHK(hipMalloc((void **)&m->d_pf_xd, sizeof(float) * nbmax * PP));
         HIPCHK(hipMalloc((void **)&m->d_pf_xc2, 32 * nbmax * PP));
         HIPCHK(hipMalloc((void **)&m->d_pf_xd2, sizeof(float) * nbmax * PP));
+        /* padding tokens of the images feed the MFMAs columns whose results are never stored: zeroed
+         * once so that they hold finite values */
         HIPCHK(hipMemsetAsync(m->d_pf_xc, 0, 32 * nbmax * PP, g_stream));
         HIPCHK(hipMemsetAsync(m->d_pf_xd, 0, sizeof(float) * nbmax * PP, g_stream));
+        HIPCHK(hipMemsetAsync(m->d_pf_xc2, 0, 32 * nbmax * PP, g_stream));
+        HIPCHK(hipMemsetAsync(m->d_pf_xd2, 0, sizeof(float) * nbmax * PP, g_stream));
     }
     HIPCHK(hipStreamSynchronize(g_stream));
     m->use_graph = getenv("QMH_NO_GRAPH") == NULL;
