@@ -281,6 +281,11 @@ class Ref:
             fn(_ptr(x[r]), out[r].ctypes.data, n)
         return out
 
+    def row_to_f32(self, dtype: int, row: np.ndarray, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        self.L.qm_row_to_f32(dtype, _ptr(np.ascontiguousarray(row)), _ptr(out), n)
+        return out
+
     def model_config(self, path: str, max_seq: int = 0):
         """(config dict, None) from the reference's own qm_model_load (src/model.c:35-117), or
         (None, its error message). qm_config is the first member of qm_model (src/model.h:17-18)."""

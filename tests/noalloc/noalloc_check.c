@@ -11,7 +11,13 @@
  * of the previous logits), then of qmh_model_greedy and qmh_model_sample over the same positions.
  * Prints one line per phase: every allocation in the process, and those libqmhip.so made itself; each
  * allocation is attributed (backtrace, dladdr) to the library function and, when the HIP runtime
- * allocated, the HIP entry point that the library called. */
+ * allocated, the HIP entry point that the library called.
+ *
+ * Then qmh_sample_noalloc, the entry point for callers that cannot allocate: after one warm-up call,
+ * 32 calls at a vocabulary above 8192 (the multi-workgroup path) and 32 at one below it, counted like
+ * the phases above, with the device's free memory (hipMemGetInfo) read before and after. Last, the
+ * same draw captured in a HIP graph (the caller it is for) and replayed 8 times, eager draws of a
+ * sampler object between the replays: each replay's token and rng state against the eager draw's. */
 #define _GNU_SOURCE
 #include <dlfcn.h>
 #include <execinfo.h>
@@ -19,6 +25,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include <hip/hip_runtime_api.h>
 
 #include "../../include/qmhip.h"
 
@@ -212,5 +220,80 @@ int main(int argc, char **argv) {
     qmh_model_free(m);
     free(out);
     printf("hot-loop heap allocations made by the library: %ld\n", total);
-    return 0;
+
+    /* qmh_sample_noalloc: logits of a fixed pseudo-random pattern, vocabularies 32000 and 4000 */
+    enum { NV = 32000, NS = 4000 };
+    float *hl = malloc(sizeof(float) * NV);
+    float *dl = qmh_dev_alloc(sizeof(float) * NV);
+    uint64_t *drng = qmh_dev_alloc(sizeof(uint64_t)), *drng2 = qmh_dev_alloc(sizeof(uint64_t));
+    int32_t *dout = qmh_dev_alloc(sizeof(int32_t)), *dout2 = qmh_dev_alloc(sizeof(int32_t));
+    if (!hl || !dl || !drng || !drng2 || !dout || !dout2) {
+        fprintf(stderr, "noalloc buffers: %s\n", qmh_last_error());
+        return 1;
+    }
+    uint64_t z = 0x2545f4914f6cdd1dull;
+    for (int i = 0; i < NV; i++) {
+        z = z * 6364136223846793005ull + 1442695040888963407ull;
+        hl[i] = (float)((int64_t)(z >> 40) - (1 << 23)) * 0x1p-20f;  /* about [-8, 8) */
+    }
+    const uint64_t seed0 = 0x9e3779b97f4a7c15ull;
+    if (qmh_memcpy_h2d(dl, hl, sizeof(float) * NV) || qmh_memcpy_h2d(drng, &seed0, sizeof seed0)) {
+        fprintf(stderr, "noalloc setup: %s\n", qmh_last_error());
+        return 1;
+    }
+    if (qmh_sample_noalloc(dl, NV, 0.8f, 0, 0.95f, drng, dout, NULL) ||
+        qmh_sample_noalloc(dl, NS, 0.8f, 0, 0.95f, drng, dout, NULL) || qmh_sync()) {
+        fprintf(stderr, "noalloc warm-up: %s\n", qmh_last_error());
+        return 1;
+    }
+    size_t free0 = 0, free1 = 0, tot = 0;
+    if (hipMemGetInfo(&free0, &tot) != hipSuccess) return 1;
+    begin();
+    rc = 0;
+    for (int k = 0; k < 32 && rc == 0; k++) rc = qmh_sample_noalloc(dl, NV, 0.8f, 0, 0.95f, drng, dout, NULL);
+    for (int k = 0; k < 32 && rc == 0; k++) rc = qmh_sample_noalloc(dl, NS, 0.8f, 0, 0.95f, drng, dout, NULL);
+    rc |= qmh_sync();
+    const long own_na = end("qmh_sample_noalloc", 64);
+    if (rc || hipMemGetInfo(&free1, &tot) != hipSuccess) {
+        fprintf(stderr, "noalloc calls: %s\n", qmh_last_error());
+        return 1;
+    }
+    printf("qmh_sample_noalloc device free bytes: before %zu after %zu (%s)\n", free0, free1,
+           free0 == free1 ? "unchanged" : "CHANGED");
+
+    /* the draw under graph capture, replayed; eager draws of a sampler object between the replays */
+    qmh_sampler *ref = qmh_sampler_create(NV, 0.8f, 0, 0.95f, 12345);
+    uint64_t r0 = 0;
+    hipStream_t st = NULL;
+    hipGraph_t g = NULL;
+    hipGraphExec_t ge = NULL;
+    if (!ref || qmh_sampler_rng(ref, &r0) || qmh_memcpy_h2d(drng2, &r0, sizeof r0) || hipStreamCreate(&st) != hipSuccess ||
+        hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        fprintf(stderr, "graph setup: %s\n", qmh_last_error());
+        return 1;
+    }
+    rc = qmh_sample_noalloc(dl, NV, 0.8f, 0, 0.95f, drng2, dout2, st);
+    if (hipStreamEndCapture(st, &g) != hipSuccess || rc || hipGraphInstantiate(&ge, g, NULL, NULL, 0) != hipSuccess) {
+        fprintf(stderr, "graph capture failed (rc %d): %s\n", rc, qmh_last_error());
+        return 1;
+    }
+    int bad = 0;
+    for (int k = 0; k < 8; k++) {
+        int32_t tg = -1, te = -1;
+        uint64_t rg = 0, re = 0;
+        if (hipGraphLaunch(ge, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return 1;
+        if (qmh_memcpy_d2h(&tg, dout2, sizeof tg) || qmh_memcpy_d2h(&rg, drng2, sizeof rg)) return 1;
+        te = qmh_sample_sync(ref, dl);
+        if (te < 0 || qmh_sampler_rng(ref, &re)) return 1;
+        printf("graph replay %d: token %d rng %016llx, eager %d rng %016llx%s\n", k, tg, (unsigned long long)rg, te,
+               (unsigned long long)re, tg == te && rg == re ? "" : "  MISMATCH");
+        bad += tg != te || rg != re;
+    }
+    hipGraphExecDestroy(ge);
+    hipGraphDestroy(g);
+    hipStreamDestroy(st);
+    qmh_sampler_free(ref);
+    printf("graph replays matching the eager draws: %d of 8\n", 8 - bad);
+    fflush(stdout);
+    return own_na || free0 != free1 || bad ? 3 : 0;
 }

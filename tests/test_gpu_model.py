@@ -252,6 +252,18 @@ def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
     # sequential forwards (the batched prompt path takes head_dim % 4 == 0 only)
     ("mha10", dict(dim=60, hidden_dim=128, n_layers=1, n_heads=6, n_kv_heads=6, vocab_size=300, max_seq=700),
      "q8_0", [(636, 646), (690, 700)]),
+    # grouped heads with head_dim 6 and 10 (not a multiple of 4): the scalar-column kernel with the
+    # group's scores in LDS (k_attn_pv<640, false>), across 256 and its 640-position chunk boundary
+    ("gqa6", dict(dim=24, hidden_dim=64, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=700),
+     "q8_0", [(250, 262), (636, 646)]),
+    ("gqa10", dict(dim=40, hidden_dim=96, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=700),
+     "q4_0", [(250, 262), (636, 646)]),
+    # 12 query heads on one kv head of 10 dims: the 256-position chunks (k_attn_pv<256, false>)
+    ("gqa10x12", dict(dim=120, hidden_dim=128, n_layers=1, n_heads=12, n_kv_heads=1, vocab_size=300, max_seq=530),
+     "q8_0", [(250, 262), (508, 516)]),
+    # one query head per kv head past 8192 positions: the chunked V sum (attn_pv_chunks<640, true>)
+    ("mha16long", dict(dim=32, hidden_dim=64, n_layers=1, n_heads=2, n_kv_heads=2, vocab_size=300, max_seq=8200),
+     "q4_0", [(8188, 8197)]),
 ])
 def test_long_context_decode_matches_oracle(gpu, oracle, tmp_path, name, dims, wt, spans):
     """Decode forwards at positions on either side of the attention kernels' chunk boundaries

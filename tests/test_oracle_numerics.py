@@ -76,6 +76,28 @@ def test_quantize_bytes_match_reference(oracle, ref, dtype):
         assert np.array_equal(oracle.quantize(dtype, x), ref.quantize(dtype, x)), n
 
 
+@pytest.mark.parametrize("dtype", [F32, Q8_0, Q4_0])
+def test_row_to_f32_bitexact_vs_reference(oracle, ref, dtype):
+    """or_row_to_f32 against the compiled qm_row_to_f32 (src/quant.c:65-101) on rows of every length
+    1..300 and 4096: quantized rows from the reference's quantizer (zero blocks, subnormal and large
+    scales), raw random bytes as codes and scales (every code value, NaN/inf/subnormal fp16 scales),
+    and f32 rows."""
+    for n in list(range(1, 301)) + [4096]:
+        if dtype == F32:
+            rows = [rng.standard_normal(n).astype(np.float32).view(np.uint8),
+                    rng.integers(0, 256, 4 * n, dtype=np.uint8)]
+        else:
+            x = _rows(n, float(np.exp2(rng.integers(-20, 20))))
+            if n % 5 == 0:
+                x[0, : min(n, 40)] = 0.0
+            q = ref.quantize(dtype, x)
+            rows = [q[0], q[1], rng.integers(0, 256, q.shape[1], dtype=np.uint8)]
+        for row in rows:
+            a, b = oracle.row_to_f32(dtype, row, n), ref.row_to_f32(dtype, row, n)
+            # NaN scales give NaN values whose payload bits are the x86 conversion's in both
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (dtype, n)
+
+
 def test_quantize_known_answers(oracle):
     # zero input -> zero scale, zero codes; Q4 byte 0x88 (reference tests/test_quant.c:61-68)
     z = np.zeros(64, np.float32)
