@@ -669,8 +669,8 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 // ============================================================================ one launch per step
 
 // The decode step's whole attention in one launch, for contexts of up to QMH_AF_TC positions:
-// workgroup (cg, h) of grid (head_dim/16, n_heads) owns query head h's output columns 16*cg ..
-// +15 (as k_attn_pv_mha) and computes the scores of a slice of the head's positions,
+// workgroup (cg, h) owns query head h's output columns 16*cg .. +15 (as k_attn_pv_mha) and
+// computes the scores of a slice of the head's positions,
 // [cg*sp, cg*sp + sp) with sp = ceil(n / (head_dim/16)) rounded up to 4. Its K slice arrives as
 // float4s of 4 positions of one dimension (all in flight together), is staged in LDS as rows of
 // head_dim + 4 floats (one position per row), and one lane per position runs the score's serial
@@ -678,15 +678,23 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 // through agent-scope atomic stores; every workgroup of the head then loads the head's n words
 // with agent-scope atomic loads until each carries this launch's epoch, and runs k_attn_pv_mha's
 // statistics and V sum on them. A word is written and read whole, so a value is taken only with
-// the epoch it was stored with: the exchange needs no barrier and no fence. The epoch of layer l is
+// the epoch it was stored with: the exchange needs no barrier and no fence.
+// The grid is one-dimensional and the dispatcher places workgroup L on XCD L % 8 (round robin
+// from XCD 0, measured on MI355X): XCD x takes heads x, x + 8, x + 16, ... (workgroups
+// L = x + 8*(j*NCG + cg)), so a head's workgroups share one L2, where a poll finds a word another
+// workgroup stored in about 120 ns (measured); across XCDs the exchange took microseconds. The
+// placement is a matter of speed only: the atomics are coherent across the device. The epoch of layer l is
 // sync[0]*n_layers + l + 1; sync[0] counts decode steps (k_embed adds one per step), so no two
 // launches of a step, nor of two steps, share one, and attp holds only older epochs when a launch
 // starts. Every wait is bounded: past `spin` polls the workgroup sets sync[1] (which the host
 // reports as an error) and goes on. skew (0 in use) makes the readers wait for an epoch nobody
-// writes, so that a test can run the bounded wait to its end from the host. The head's workgroups are consecutive in dispatch order
-// (blockIdx.x fastest) and the host launches at most as many workgroups as the device holds at once.
+// writes, so that a test can run the bounded wait to its end from the host. The host launches at
+// most as many workgroups as the device holds at once.
 #define QMH_AF_TC 640
 #define QMH_AF_SPIN (1u << 16)
+// workgroups of k_attn_fused's grid: 8 XCDs x ceil(n_heads / 8) heads x head_dim/16
+__host__ __device__ __forceinline__ int af_grid(int n_heads, int hd) { return 8 * ((n_heads + 7) / 8) * (hd / QMH_PV_CW); }
+
 template <int HD>
 __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ Kt,
                                                        const float *__restrict__ V, float *__restrict__ out,
@@ -704,12 +712,14 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
     __shared__ float x0s;
     const int n = *pos_ptr + 1;
     if (n < 1 || n > TC || n > max_seq) {  // the host takes longer contexts elsewhere: flag a stray launch
-        if (n > TC && n <= max_seq && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+        if (n > TC && n <= max_seq && blockIdx.x == 0 && threadIdx.x == 0)
             __hip_atomic_store(sync + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     const int tid = threadIdx.x;
-    const int cg = blockIdx.x, h = blockIdx.y, kvh = h / (n_heads / n_kv), kvd = HD * n_kv, i0 = cg * CW;
+    const int xj = (int)(blockIdx.x >> 3), h = (int)(blockIdx.x & 7) + 8 * (xj / NCG), cg = xj % NCG;
+    if (h >= n_heads) return;  // the grid rounds the heads up to a multiple of 8
+    const int kvh = h / (n_heads / n_kv), kvd = HD * n_kv, i0 = cg * CW;
     const uint32_t ep = sync[0] * (uint32_t)n_layers + (uint32_t)layer + 1u, want = ep + skew;
     const int sp = ((n + NCG - 1) / NCG + 3) & ~3, p0 = cg * sp;
     const int np = (n - p0 < sp ? n - p0 : sp) > 0 ? (n - p0 < sp ? n - p0 : sp) : 0;  // positions of the slice
@@ -841,7 +851,7 @@ extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_di
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, QMH_WG, af_lds_bytes(head_dim)) != hipSuccess)
         return 0;
-    return (long long)(head_dim / QMH_PV_CW) * n_heads <= (long long)per * ncu;
+    return (long long)af_grid(n_heads, head_dim) <= (long long)per * ncu;
 }
 
 // the caller has checked qmh_attn_fused_supported for the shape; stall != 0 (tests only): the
@@ -853,7 +863,7 @@ extern "C" int qmh_launch_attn_fused(const float *q, const float *kcache, const 
     if ((head_dim != 128 && head_dim != 64 && head_dim != 48) || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 ||
         n_heads % n_kv_heads)
         return (int)hipErrorNotSupported;
-    const dim3 grid(head_dim / QMH_PV_CW, n_heads);
+    const dim3 grid(af_grid(n_heads, head_dim));
     const size_t lds = af_lds_bytes(head_dim);
     hipStream_t s = (hipStream_t)stream;
     const uint32_t spin = stall ? 64u : QMH_AF_SPIN, skew = stall ? 1u : 0u;

@@ -222,7 +222,8 @@ def af_lds_floats(hd):
 
 
 def fused(nh, nkv, hd, S, n, ext):
-    """k_attn_fused<HD> over grid (hd/16, nh) x 256 threads, n <= 640 positions: every thread loads its
+    """k_attn_fused<HD> over its (head, column group) workgroups x 256 threads (the grid's placement:
+    af_grid_map), n <= 640 positions: every thread loads its
     part of the K slice and its V float4s (as k_attn_pv_mha), the threads below the slice's position
     count run the score chains, every thread reads the head's scores, stages its products for all 640
     positions, and the first 16 threads run the V sum's chains (pv_short_flow)."""
@@ -324,6 +325,31 @@ def test_fused_slices_cover_every_position():
         ext = Extents(2, 1, hd, 640)
         for n in range(1, AF_TC + 1):
             fused(2, 1, hd, 640, n, ext)
+
+
+def af_grid_map(nh, hd):
+    """k_attn_fused's one-dimensional grid: 8 * ceil(nh/8) * (hd/16) workgroups; workgroup L takes
+    head (L % 8) + 8 * ((L / 8) / ncg), column group (L / 8) % ncg, and returns when the head is past
+    nh. (h, cg) of each workgroup, -1 for the ones that return."""
+    ncg = hd // CW
+    G = 8 * ((nh + 7) // 8) * ncg
+    L = np.arange(G)
+    h = (L & 7) + 8 * ((L >> 3) // ncg)
+    cg = (L >> 3) % ncg
+    return L, np.where(h < nh, h, -1), np.where(h < nh, cg, -1)
+
+
+@pytest.mark.parametrize("nh", [1, 2, 4, 6, 8, 12, 25, 32, 64])
+@pytest.mark.parametrize("hd", [48, 64, 128])
+def test_fused_grid_places_each_head_on_one_xcd(nh, hd):
+    """Every (head, column group) has exactly one workgroup, and a head's workgroups have one
+    dispatch slot modulo 8 (the XCD the round-robin dispatcher gives them)."""
+    L, h, cg = af_grid_map(nh, hd)
+    live = h >= 0
+    pairs = h[live] * (hd // CW) + cg[live]
+    assert np.array_equal(np.sort(pairs), np.arange(nh * (hd // CW)))
+    for head in range(nh):
+        assert len(set((L[h == head] % 8).tolist())) == 1
 
 
 def test_model_catches_an_out_of_range_clamp():
