@@ -737,9 +737,10 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
         kv[k] = qmh_ld_nt4(kb + (size_t)d * max_seq + tc);
     }
     const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
-    // V (position k*64 + tid/4, columns c .. c+3), loaded non-temporally after K has arrived: loads
-    // issued together with K's delay it, and a wave that issues loads before its chain stalls in
-    // its chain. The waves without chain lanes issue theirs at once, the others after their chains.
+    // V (position k*64 + tid/4, columns c .. c+3), loaded non-temporally right behind K: K's
+    // arrival waits only for K (the vector-memory counter retires loads in order), and the barrier
+    // after the K slice's staging waits for LDS alone, so V streams under the score chains and the
+    // poll (measured on MI355X: the poll's results come back behind V either way)
     const int c = i0 + 4 * (tid & 3), cc = c <= HD - 4 ? c : HD - 4;
     float4 vv[L4];
     auto vload = [&] {
@@ -749,6 +750,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
             vv[k] = qmh_ld_nt4(V + (size_t)tcl * kvd + (size_t)kvh * HD + cc);
         }
     };
+    vload();
     // the slice in LDS, row r = position p0 + r
     float *kt = af_smem;
     if (tid < HD / 4) ((float4 *)qs)[tid] = q4;
@@ -763,10 +765,7 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
             kt[(r + 3) * KS + d] = kv[k].w;
         }
     }
-    __syncthreads();
-    // wave-uniform: does this wave hold chain lanes?
-    const bool chain_wave = (tid & ~63) < np;
-    if (!chain_wave) vload();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the slice and q in LDS
     // scores: s = +0; s = s + q[i]*k[i] in dimension order, times scale (src/model.c:142-146); the
     // row and q are read from LDS eight float4s ahead of their products
     uint64_t *row = attp + (size_t)h * max_seq;
@@ -795,15 +794,13 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
         __hip_atomic_store(row + p0 + tid, ((uint64_t)ep << 32) | __float_as_uint(sc), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-    // the head's n scores, each once it carries this launch's epoch (the first loads go out before a
-    // chain wave's V loads, so waiting for them does not wait for V)
+    // the head's n scores, each once it carries this launch's epoch
     uint64_t w[SK];
 #pragma unroll
     for (int k = 0; k < SK; k++) {
         const int t = tid + k * QMH_WG;
         w[k] = t < n ? __hip_atomic_load(row + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)want << 32;
     }
-    if (chain_wave) vload();
     for (uint32_t it = 0;; it++) {
         bool ok = true;
 #pragma unroll

@@ -57,6 +57,7 @@ typedef struct {
     const float *rope; /* [max_seq][head_dim/2][2] (cos, sin) */
     const int32_t *pos_ptr;
     int head_dim, max_seq, kvd;
+    int exact_norm; /* tests: the RMSNorm always takes the serial sum of squares */
 } qmh_mv_args;
 
 /* nslots: slots the codes/scales allocation holds; slots at or past it are never written */

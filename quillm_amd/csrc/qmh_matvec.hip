@@ -158,10 +158,11 @@ __device__ void act_finish(const qmh_mv_args &a, const float4 *xr, const float4 
 #pragma unroll
         for (int w = 0; w < NT / 64; w++) ss += red[w];
         // same ss in every thread: uniform branches
-        if (!qmh_rms_inv_margin(ss, n, nb * 32, a.eps, &inv)) {
+        // (a.exact_norm, tests: always the serial sum)
+        if (a.exact_norm || !qmh_rms_inv_margin(ss, n, nb * 32, a.eps, &inv)) {
             const double d = qmh_sum_slack(ss, nb * 32);
             inv = qmh_rms_inv(ss - d, n, a.eps);
-            if (inv != qmh_rms_inv(ss + d, n, a.eps)) {
+            if (a.exact_norm || inv != qmh_rms_inv(ss + d, n, a.eps)) {
                 if (tid == 0) {
                     double s = 0.0;
                     for (int i = 0; i < n; i++) s += (double)a.x[i] * (double)a.x[i];

@@ -311,8 +311,13 @@ void qmh_weight_free(qmh_weight *w) {
     free(w);
 }
 
+/* QMH_EXACT_NORM (tests), read when a model loads: the matvecs' RMSNorms always take the serial
+ * sum of squares, the path a failed certificate takes */
+static int g_exact_norm;
+
 static void mv_args_for(const struct qmh_weight *w, qmh_mv_args *a) {
     memset(a, 0, sizeof *a);
+    a->exact_norm = g_exact_norm;
     a->dtype = w->dtype;
     a->codes = w->codes;
     a->scales = w->scales;
@@ -806,11 +811,16 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     if (e != hipSuccess) return fail("rope table: %s", hipGetErrorString(e));
 
     /* activations and caches (zeroed like the reference's arena, src/arena.c:6-15) */
+    g_exact_norm = getenv("QMH_EXACT_NORM") != NULL;
     const size_t kv_bytes = sizeof(float) * (size_t)c->n_layers * (size_t)S_ * (size_t)KV;
     HIPCHK(hipMalloc((void **)&m->d_x, sizeof(float) * D));
     HIPCHK(hipMalloc((void **)&m->d_xb, sizeof(float) * D));
     HIPCHK(hipMalloc((void **)&m->d_q, sizeof(float) * D));
     HIPCHK(hipMalloc((void **)&m->d_hb, sizeof(float) * 2 * H));
+    HIPCHK(hipMemsetAsync(m->d_x, 0, sizeof(float) * D, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_xb, 0, sizeof(float) * D, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_q, 0, sizeof(float) * D, g_stream));
+    HIPCHK(hipMemsetAsync(m->d_hb, 0, sizeof(float) * 2 * H, g_stream));
     HIPCHK(hipMalloc(&m->d_hq, QMH_XQ_IMAGE_BYTES((H + 31) / 32)));
     HIPCHK(hipMemsetAsync(m->d_hq, 0, QMH_XQ_IMAGE_BYTES((H + 31) / 32), g_stream)); /* the pad reads as 0 */
     HIPCHK(hipMalloc((void **)&m->d_att, sizeof(float) * (size_t)c->n_heads * S_));

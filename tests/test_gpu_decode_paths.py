@@ -10,6 +10,8 @@
   model, tests/test_threads.c:56-94 compares thread counts bitwise).
 * The bounded wait of the one-launch attention, run to its end from the host (QMH_AF_FORCE_STALL):
   the call fails with a message instead of returning logits.
+* Every RMSNorm of the matvecs on its serial path (QMH_EXACT_NORM: the sum of squares a failed
+  certificate recomputes in the reference's order) against the oracle.
 """
 import os
 import sys
@@ -180,4 +182,17 @@ def test_fused_attention_stage_timer(gpu, oracle, af_models):
             assert ms > 0 and nbytes == 0
         m.prefill(prompt, 0)  # the timer wrote the caches at its positions
         ids = m.greedy(int(want_ids[0]), len(prompt), 4)
+    assert list(ids) == list(want_ids[1:])
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+def test_exact_norm_path_matches_oracle(gpu, oracle, af_models, wt):
+    path = af_models[("af64g", wt)]
+    P, G = 24, 6
+    prompt = gpu.prompt_ids(P, 300, seed=14)
+    want, want_ids = oracle.run_model(path, prompt, n_gen=G)
+    say(f"case exact norm {wt}")
+    first, lg, ids = decode(gpu, path, prompt, G, QMH_EXACT_NORM="1")
+    assert first == int(want_ids[0])
+    assert np.array_equal(bits(lg), bits(want[P:]))
     assert list(ids) == list(want_ids[1:])
