@@ -251,43 +251,14 @@ namespace {
 
 // first index of the maximum of row blockIdx.x (src/sampler.c:27-32), then the sequence's next
 // token and position for the device greedy loop; record[step*B + b] = idx when record != NULL
+template <bool VEC>
 __global__ __launch_bounds__(1024) void k_bt_argmax(const float *__restrict__ logits, int V, int32_t *tok,
                                                     int32_t *pos, int32_t *record, int step) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     const int b = blockIdx.x, B = gridDim.x;
-    const float *x = logits + (size_t)b * V;
-    float v = -__builtin_inff();
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) {
-        const float xv = x[i];
-        if (xv == xv && (idx == 0x7fffffff || xv > v)) {
-            v = xv;
-            idx = i;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o);
-        const int oi = __shfl_xor(idx, o);
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
-    }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        bv[w] = v;
-        bi[w] = idx;
-    }
-    __syncthreads();
+    const int idx = qmh_block_argmax<VEC>(logits + (size_t)b * V, V, bv, bi);
     if (threadIdx.x == 0) {
-        for (int k = 1; k < (int)(blockDim.x >> 6); k++)
-            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
-                v = bv[k];
-                idx = bi[k];
-            }
-        if (idx == 0x7fffffff || x[0] != x[0]) idx = 0;  // all NaN, or NaN at 0
         tok[b] = idx;
         pos[b] += 1;
         if (record) record[(size_t)step * B + b] = idx;
@@ -298,6 +269,12 @@ __global__ __launch_bounds__(1024) void k_bt_argmax(const float *__restrict__ lo
 
 extern "C" int qmh_launch_bt_argmax(const float *logits, int B, int V, int32_t *tok, int32_t *pos, int32_t *record,
                                     int step, void *stream) {
-    hipLaunchKernelGGL(k_bt_argmax, dim3(B), dim3(1024), 0, (hipStream_t)stream, logits, V, tok, pos, record, step);
+    // 16-byte loads when every row starts 16-byte aligned
+    if (((uintptr_t)logits & 15) == 0 && (V % 4 == 0 || B == 1))
+        hipLaunchKernelGGL(k_bt_argmax<true>, dim3(B), dim3(1024), 0, (hipStream_t)stream, logits, V, tok, pos, record,
+                           step);
+    else
+        hipLaunchKernelGGL(k_bt_argmax<false>, dim3(B), dim3(1024), 0, (hipStream_t)stream, logits, V, tok, pos,
+                           record, step);
     return (int)hipGetLastError();
 }

@@ -312,3 +312,81 @@ __device__ __forceinline__ int qmh_sum8(int v) {
     v += qmh_dpp<QMH_DPP_QXOR2>(v);
     return v + qmh_dpp<QMH_DPP_HALF_MIRROR>(v);
 }
+
+// First index of the maximum of x[0..n) over the whole workgroup (src/sampler.c:27-32: `if (x[i] >
+// x[best]) best = i` from best = 0, so a NaN at 0 wins and NaNs elsewhere are never chosen). Each
+// thread walks its elements in increasing index order keeping the first strict maximum of the
+// non-NaN values, with up to 8 loads in flight per round (VEC: 16-byte loads, x 16-byte aligned,
+// so 32768 values take one round of 1024 threads); pairs then combine preferring the larger value,
+// then the lower index, and a NaN x[0] overrides the result. The result is valid in thread 0.
+template <bool VEC>
+__device__ __forceinline__ int qmh_block_argmax(const float *__restrict__ x, int n, float *bv, int *bi) {
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    auto take = [&](float xv, int i) {
+        if (xv == xv && (idx == 0x7fffffff || xv > v)) {
+            v = xv;
+            idx = i;
+        }
+    };
+    const int nt = (int)blockDim.x;
+    if (VEC) {
+        const int n4 = n >> 2;
+        const float4 *x4 = (const float4 *)x;
+        for (int i0 = (int)threadIdx.x; i0 < n4; i0 += 8 * nt) {
+            float4 xv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + k * nt;
+                xv[k] = x4[i < n4 ? i : 0];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + k * nt;
+                if (i < n4) {
+                    take(xv[k].x, 4 * i);
+                    take(xv[k].y, 4 * i + 1);
+                    take(xv[k].z, 4 * i + 2);
+                    take(xv[k].w, 4 * i + 3);
+                }
+            }
+        }
+        if ((int)threadIdx.x < (n & 3)) take(x[4 * n4 + (int)threadIdx.x], 4 * n4 + (int)threadIdx.x);
+    } else {
+        for (int i0 = (int)threadIdx.x; i0 < n; i0 += 8 * nt) {
+            float xv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + k * nt;
+                xv[k] = x[i < n ? i : 0];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (i0 + k * nt < n) take(xv[k], i0 + k * nt);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(idx, o);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    const int w = (int)threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[w] = v;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < nt >> 6; k++)
+            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
+                v = bv[k];
+                idx = bi[k];
+            }
+        if (idx == 0x7fffffff || x[0] != x[0]) idx = 0;  // all NaN, or NaN at 0
+    }
+    return idx;
+}

@@ -46,55 +46,16 @@ extern "C" int qmh_launch_embed(const uint8_t *tok_embd, int dtype, int dim, int
 
 // ============================================================================ argmax
 
-// first index of the maximum (src/sampler.c:27-32): `if (x[i] > x[best]) best = i` from best = 0,
-// so a NaN at 0 wins and NaNs elsewhere are never chosen. Each thread keeps the first strict
-// maximum of the non-NaN values of its stride (8 loads in flight per round), pairs combine
-// preferring the larger value, then the lower index, and a NaN x[0] overrides the result.
+// argmax over x[n] (qmh_block_argmax, one workgroup of 1024 threads; 16-byte loads when x is 16-byte
+// aligned), with the decode loop's bookkeeping when tokpos != NULL: tokpos[0] = the token,
+// tokpos[1] += 1, record[tokpos[2]] = it, tokpos[2] += 1
+template <bool VEC>
 __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n, int32_t *out_idx,
                                                  int32_t *tokpos, int32_t *record, int record_cap) {
     __shared__ float bv[16];
     __shared__ int bi[16];
-    float v = -__builtin_inff();
-    int idx = 0x7fffffff;
-    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
-        float xv[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = i0 + k * (int)blockDim.x;
-            xv[k] = x[i < n ? i : 0];
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = i0 + k * (int)blockDim.x;
-            if (i < n && xv[k] == xv[k] && (idx == 0x7fffffff || xv[k] > v)) {
-                v = xv[k];
-                idx = i;
-            }
-        }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(v, o);
-        int oi = __shfl_xor(idx, o);
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
-    }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        bv[w] = v;
-        bi[w] = idx;
-    }
-    __syncthreads();
+    const int idx = qmh_block_argmax<VEC>(x, n, bv, bi);
     if (threadIdx.x == 0) {
-        const int nw = blockDim.x >> 6;
-        for (int k = 1; k < nw; k++)
-            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
-                v = bv[k];
-                idx = bi[k];
-            }
-        if (idx == 0x7fffffff || x[0] != x[0]) idx = 0;  // all NaN, or NaN at 0
         if (out_idx) *out_idx = idx;
         if (tokpos) {
             tokpos[0] = idx;
@@ -108,8 +69,12 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, in
 
 extern "C" int qmh_launch_argmax(const float *x, int n, int32_t *out_idx, int32_t *tokpos, int32_t *record,
                                  int record_cap, void *stream) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos, record,
-                       record_cap);
+    if (((uintptr_t)x & 15) == 0)
+        hipLaunchKernelGGL(k_argmax<true>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos,
+                           record, record_cap);
+    else
+        hipLaunchKernelGGL(k_argmax<false>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, n, out_idx, tokpos,
+                           record, record_cap);
     return (int)hipGetLastError();
 }
 

@@ -291,3 +291,23 @@ def test_argmax_nan_and_inf_semantics(gpu, oracle):
         x = np.asarray(c, np.float32)
         gpu._check(L.qmh_argmax(dev(gpu, x).ptr, x.size, di.ptr, None), "argmax")
         assert di.to_array(np.int32)[0] == oracle.argmax(x), c[:6]
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 31999, 32000, 32001, 32768, 32771, 100003])
+def test_argmax_vector_and_scalar_loads(gpu, oracle, n):
+    """16-byte loads from an aligned vector (with the n % 4 tail), 4-byte loads from one that starts
+    4 bytes past a 16-byte boundary: the same first index of the maximum, NaNs and ties included."""
+    L = gpu.load_library()
+    r = np.random.default_rng(n)
+    x = r.standard_normal(n).astype(np.float32)
+    x[r.integers(0, n, size=max(1, n // 50))] = np.float32(np.nan)
+    top = r.integers(0, n, size=3)
+    x[top] = np.float32(9.0)  # ties: the lowest of these indices wins unless it is NaN'd below
+    if n > 8:
+        x[top[0]] = np.float32(np.nan)
+    di = gpu.DeviceBuffer(4)
+    gpu._check(L.qmh_argmax(dev(gpu, x).ptr, n, di.ptr, None), "argmax")
+    assert di.to_array(np.int32)[0] == oracle.argmax(x)
+    padded = dev(gpu, np.concatenate([np.zeros(1, np.float32), x]))
+    gpu._check(L.qmh_argmax(padded.ptr + 4, n, di.ptr, None), "argmax")
+    assert di.to_array(np.int32)[0] == oracle.argmax(x)
