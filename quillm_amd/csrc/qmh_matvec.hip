@@ -626,31 +626,38 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
 }
 
 // f32 weights (src/kernels_scalar.c:6-10 via src/ops.c:42-45): s = +0; s = s + w_i*x_i in index
-// order, one lane per row. A workgroup owns MF_R consecutive rows. Their weights stream through LDS
-// in chunks of MF_C columns, coalesced (64 consecutive threads read 1 KB of one row). The activation (RMSNorm'd when a gain is given, as the reference's
-// (x*inv)*w) sits in LDS for every chunk. Up to three chunks are ahead of the chains: one in LDS,
-// two in registers.
+// order, one lane per row. A workgroup owns MF_R consecutive rows and has MF_NL loader threads plus
+// one chain wave. The weights stream in chunks of MF_C columns, coalesced (64 consecutive loader
+// threads read 1 KB of one row), two chunks ahead in registers. The loaders turn a chunk into its
+// products w_i*x_i (the reference's multiply, rounded alone) and stage them in LDS, one of two
+// buffers, while the chain wave's first MF_R lanes add the previous chunk's products in index
+// order, 32 per step, with the next 32 already read from LDS. The activation (RMSNorm'd when a gain
+// is given, as the reference's (x*inv)*w) sits in LDS for every chunk. One barrier per chunk. The
+// chains bound the kernel: a dependent add fed from LDS takes ~10 clocks, so 4096 columns ~17 us.
 #define MF_R 16
 #define MF_C 256
-#define MF_L4 (MF_R * MF_C / 4 / QMH_WG)  // float4 loads per thread per chunk
-__global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
-    static_assert(MF_L4 * QMH_WG * 4 == MF_R * MF_C && MF_C % 4 == 0, "whole float4 chunks");
+#define MF_NL 512                         // loader threads (waves 0-7); wave 8 runs the chains
+#define MF_NT (MF_NL + 64)
+#define MF_L4 (MF_R * MF_C / 4 / MF_NL)  // float4 loads per loader thread per chunk
+__global__ __launch_bounds__(MF_NT) void k_matvec_f32(qmh_mv_args a) {
+    static_assert(MF_L4 * MF_NL * 4 == MF_R * MF_C && MF_C % 64 == 0 && MF_R <= 64, "whole float4 chunks");
     constexpr int TS = MF_C + 4;  // LDS row stride of a chunk (== 4 mod 64 floats)
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[16];
     float *xs = (float *)smem;                                    // [cols rounded up to MF_C]
     const int n = a.cols, nch = (n + MF_C - 1) / MF_C, tid = threadIdx.x;
-    float *tile = xs + (size_t)nch * MF_C;                        // [2][MF_R][TS]
+    const bool loader = tid < MF_NL, chain = tid >= MF_NL && tid < MF_NL + MF_R;
+    float *tile = xs + (size_t)nch * MF_C;                        // [2][MF_R][TS] products
     const int r0 = blockIdx.x * MF_R;
-    // chunk c's loads: float4 f = k*QMH_WG + tid is row f / (MF_C/4), columns 4*(f % (MF_C/4)) ..; rows
+    // chunk c's loads: float4 f = k*MF_NL + tid is row f / (MF_C/4), columns 4*(f % (MF_C/4)) ..; rows
     // past the matrix re-read its last row, columns past n read the row's last whole float4 (or,
-    // for n % 4 != 0, element by element; the chain stops at n either way)
+    // for n % 4 != 0, element by element); the chains stop at n, so those products are never added
     const float *W = (const float *)a.codes;
     float4 ld[2][MF_L4];
     auto issue = [&](int c, float4(&d)[MF_L4]) {
 #pragma unroll
         for (int k = 0; k < MF_L4; k++) {
-            const int f = k * QMH_WG + tid, rr = f / (MF_C / 4), col = c * MF_C + 4 * (f % (MF_C / 4));
+            const int f = k * MF_NL + tid, rr = f / (MF_C / 4), col = c * MF_C + 4 * (f % (MF_C / 4));
             const int row = r0 + rr < a.rows ? r0 + rr : a.rows - 1;
             const float *wr = W + (size_t)row * n;
             if ((n & 3) == 0) {
@@ -663,20 +670,29 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
             }
         }
     };
-    auto stash = [&](const float4(&d)[MF_L4], float *t) {
+    // chunk c's products into buffer t (xs is zero past n)
+    auto stash = [&](int c, const float4(&d)[MF_L4], float *t) {
 #pragma unroll
         for (int k = 0; k < MF_L4; k++) {
-            const int f = k * QMH_WG + tid;
-            *(float4 *)(t + (f / (MF_C / 4)) * TS + 4 * (f % (MF_C / 4))) = d[k];
+            const int f = k * MF_NL + tid, c4 = 4 * (f % (MF_C / 4));
+            const float4 x4 = *(const float4 *)(xs + (size_t)c * MF_C + c4);
+            float4 p;
+            p.x = d[k].x * x4.x;
+            p.y = d[k].y * x4.y;
+            p.z = d[k].z * x4.z;
+            p.w = d[k].w * x4.w;
+            *(float4 *)(t + (f / (MF_C / 4)) * TS + c4) = p;
         }
     };
-    issue(0, ld[0]);
-    if (nch > 1) issue(1, ld[1]);
+    if (loader) {
+        issue(0, ld[0]);
+        if (nch > 1) issue(1, ld[1]);
+    }
     // the activation, normalised as the reference does when a gain is given (src/ops.c:93-98)
     float inv = 1.0f;
     if (a.norm_w) {
         double ss = 0.0;
-        for (int i = tid; i < n; i += QMH_WG) {
+        for (int i = tid; i < n; i += MF_NT) {
             const double v = (double)a.x[i];
             ss += v * v;
         }
@@ -687,44 +703,66 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
             if (tid == 0) {
                 double sr = 0.0;
                 for (int i = 0; i < n; i++) sr += (double)a.x[i] * (double)a.x[i];
-                red[8] = sr;
+                red[15] = sr;
             }
             __syncthreads();
-            inv = qmh_rms_inv(red[8], n, a.eps);
+            inv = qmh_rms_inv(red[15], n, a.eps);
         }
     }
-    for (int i = tid; i < nch * MF_C; i += QMH_WG)
+    for (int i = tid; i < nch * MF_C; i += MF_NT)
         xs[i] = i < n ? (a.norm_w ? a.x[i] * inv * a.norm_w[i] : a.x[i]) : 0.0f;
-    stash(ld[0], tile);
-    if (nch > 2) issue(2, ld[0]);
+    __syncthreads();
+    if (loader) {
+        stash(0, ld[0], tile);
+        if (nch > 2) issue(2, ld[0]);
+    }
     __syncthreads();
     float s = 0.0f;
-    // chunk k is loaded into registers ld[k % 2]. Step c: the chains add chunk c from LDS buffer
-    // c % 2, chunk c+1 (registers nxt) goes to LDS buffer (c+1) % 2 once it lands (the waves without
-    // chain lanes do so while the chains add), then those registers take chunk c+3 (unrolled by two:
-    // the register buffers are indexed statically)
+    // step c: the chains add chunk c from buffer c % 2 while the loaders stage chunk c+1 (registers
+    // ld[(c+1) % 2]) into buffer (c+1) % 2 and refill those registers with chunk c+3 (unrolled by
+    // two: the register sets are indexed statically)
     auto step = [&](int c, float4(&nxt)[MF_L4]) {
         const int b = c & 1;
-        if (tid < MF_R) {
-            const float4 *wr = (const float4 *)(tile + (size_t)b * MF_R * TS + tid * TS);
-            const float4 *xr = (const float4 *)(xs + (size_t)c * MF_C);
+        if (chain) {
+            const float *pr = tile + (size_t)b * MF_R * TS + (size_t)(tid - MF_NL) * TS;
             const int m = n - c * MF_C < MF_C ? n - c * MF_C : MF_C;
             if (m == MF_C) {
-#pragma unroll 8
-                for (int j = 0; j < MF_C / 4; j++) {
-                    const float4 w4 = wr[j], x4 = xr[j];
-                    s = s + w4.x * x4.x;
-                    s = s + w4.y * x4.y;
-                    s = s + w4.z * x4.z;
-                    s = s + w4.w * x4.w;
+                // 32 products per read set from two register sets: the reads of set st+1 go out
+                // before the adds of set st (the scheduling barriers keep them there), so each
+                // set waits only for reads issued a set earlier
+                const float4 *p4 = (const float4 *)pr;
+                float4 A[8], B[8];
+                auto rd = [&](float4(&d)[8], int st) {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) d[q] = p4[8 * st + q];
+                };
+                auto add = [&](const float4(&d)[8]) {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        s = s + d[q].x;
+                        s = s + d[q].y;
+                        s = s + d[q].z;
+                        s = s + d[q].w;
+                    }
+                };
+                rd(A, 0);
+#pragma unroll 1
+                for (int st = 0; st < MF_C / 32; st += 2) {
+                    rd(B, st + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    add(A);
+                    __builtin_amdgcn_sched_barrier(0);
+                    rd(A, st + 2 < MF_C / 32 ? st + 2 : st);  // the last pair re-reads a set: no branch
+                    __builtin_amdgcn_sched_barrier(0);
+                    add(B);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            } else {
-                const float *w1 = (const float *)wr, *x1 = (const float *)xr;
-                for (int j = 0; j < m; j++) s = s + w1[j] * x1[j];
+            } else {  // the last chunk, ragged
+                for (int j = 0; j < m; j++) s = s + pr[j];
             }
         }
-        if (c + 1 < nch) {
-            stash(nxt, tile + (size_t)(b ^ 1) * MF_R * TS);
+        if (loader && c + 1 < nch) {
+            stash(c + 1, nxt, tile + (size_t)(b ^ 1) * MF_R * TS);
             if (c + 3 < nch) issue(c + 3, nxt);
         }
         __syncthreads();
@@ -733,10 +771,13 @@ __global__ __launch_bounds__(QMH_WG) void k_matvec_f32(qmh_mv_args a) {
         step(c, ld[1]);
         if (c + 1 < nch) step(c + 1, ld[0]);
     }
-    const int row = r0 + (tid & (MF_R - 1));
+    // the chain wave's lanes hold rows r0 + lane (lane < MF_R)
+    const int lane = tid & 63, row = r0 + (lane & (MF_R - 1));
     const int pos = a.pos_ptr ? *a.pos_ptr : 0;
-    const EpiIn e = epi_fetch(a, row, pos);
-    if (tid < 64) mv_epilogue(a, tid < MF_R ? row : a.rows, s, tid & (MF_R - 1), MF_R, pos, e, qmh_exp2_tab);
+    if (tid >= MF_NL) {
+        const EpiIn e = epi_fetch(a, row, pos);
+        mv_epilogue(a, lane < MF_R ? row : a.rows, s, lane & (MF_R - 1), MF_R, pos, e, qmh_exp2_tab);
+    }
 }
 
 extern "C" int qmh_matvec_max_cols(int norm) {
@@ -787,6 +828,6 @@ static size_t mf_lds_bytes(int cols) {
 extern "C" int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream) {
     if (a->rows < 1 || a->cols < 1 || mf_lds_bytes(a->cols) > 160 * 1024 - 1024) return (int)hipErrorInvalidValue;
     const int grid = (a->rows + MF_R - 1) / MF_R;
-    hipLaunchKernelGGL(k_matvec_f32, dim3(grid), dim3(QMH_WG), mf_lds_bytes(a->cols), (hipStream_t)stream, *a);
+    hipLaunchKernelGGL(k_matvec_f32, dim3(grid), dim3(MF_NT), mf_lds_bytes(a->cols), (hipStream_t)stream, *a);
     return (int)hipGetLastError();
 }

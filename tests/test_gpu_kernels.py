@@ -123,6 +123,12 @@ def test_matvec_model_shapes(gpu, oracle, dtype, rows, cols):
     _matvec_case(gpu, oracle, dtype, rows, cols, scale=0.02)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (288, 768), (700, 5000), (33, 4099), (17, 257)])
+def test_matvec_f32_shapes(gpu, oracle, rows, cols):
+    """f32 weights over several 256-column chunks: whole chunks, a ragged last chunk, n % 4 != 0."""
+    _matvec_case(gpu, oracle, F32, rows, cols, scale=0.02)
+
+
 def test_gemm_nt(gpu, oracle):
     L = gpu.load_library()
     shapes = [(4, 4, 8), (512, 512, 512), (17, 130, 600), (1, 1, 1), (40, 150, 257)]
