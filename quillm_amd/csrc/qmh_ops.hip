@@ -279,38 +279,126 @@ extern "C" int qmh_launch_rope(float *v, int64_t n_heads, int64_t head_dim, cons
 }
 
 // gemm_nt in the scalar ISA's order (src/gemm_driver.h:7-28): per element, K is cut into
-// panels of 256 (QM_GEMM_KC, src/kernels.h:37); each panel is a serial fp32 sum from +0 and
-// the panel sums are added to C (from +0) in order. 16x16 outputs per workgroup, panels of A
-// and B staged in LDS (padded rows: conflict-free column walks).
+// panels of 256 (QM_GEMM_KC, src/kernels.h:37); each panel is a serial fp32 sum from +0 (each
+// product rounded alone, then added) and the panel sums are added to C (from +0) in order.
+// A workgroup of 256 threads owns 32x32 outputs, each thread a 2x2 block (four chains). A and B
+// pass through LDS in slices of GN_KS values of k, stored k-major ([k][row], rows padded to 34 so
+// the transposing writes are conflict-free and the float2 reads aligned); per k a thread reads two
+// float2 (its rows' A, its columns' B: the wave's four row pairs are broadcast reads) for four
+// multiplies and four adds. The next slice's global loads are in flight while a slice is summed.
+// Elements past M, N or K are staged as 0 and never added or stored.
 #define QMH_GEMM_KC 256
+#define GN_T 32   // outputs per workgroup side
+#define GN_KS 128  // k per LDS slice (divides QMH_GEMM_KC; a multiple of 32)
+#define GN_NQ (GN_KS / 32)  // float4 loads per thread per operand and slice
+#define GN_LD 34  // LDS row stride (floats)
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_gemm_nt(const float *__restrict__ A, const float *__restrict__ B,
                                                  float *__restrict__ C, int64_t M, int64_t N, int64_t K) {
-    __shared__ float As[16][QMH_GEMM_KC + 1], Bs[16][QMH_GEMM_KC + 1];
-    const int ty = threadIdx.x / 16, tx = threadIdx.x % 16;
-    const int64_t i = (int64_t)blockIdx.y * 16 + ty, j = (int64_t)blockIdx.x * 16 + tx;
-    float c = 0.0f;
-    for (int64_t k0 = 0; k0 < K; k0 += QMH_GEMM_KC) {
-        const int kc = (int)(K - k0 < QMH_GEMM_KC ? K - k0 : QMH_GEMM_KC);
-        for (int e = threadIdx.x; e < 16 * kc; e += 256) {
-            const int r = e / kc, k = e % kc;
-            const int64_t ai = (int64_t)blockIdx.y * 16 + r, bj = (int64_t)blockIdx.x * 16 + r;
-            As[r][k] = ai < M ? A[ai * K + k0 + k] : 0.0f;
-            Bs[r][k] = bj < N ? B[bj * K + k0 + k] : 0.0f;
+    static_assert(QMH_GEMM_KC % GN_KS == 0 && GN_T * GN_KS == 4 * 256 * GN_NQ, "whole float4s per thread per slice");
+    __shared__ __align__(16) float As[GN_KS][GN_LD], Bs[GN_KS][GN_LD];
+    const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;  // rows 2r, 2r+1; columns 2c, 2c+1
+    const int64_t i0 = (int64_t)blockIdx.y * GN_T, j0 = (int64_t)blockIdx.x * GN_T;
+    // staging: thread t loads row t/8 of the tile, k 32*q + 4*(t%8) .. +3 of the slice (q < GN_NQ),
+    // for A and for B
+    const int sr = tid >> 3, sk = 4 * (tid & 7);
+    const float *ar = A + (i0 + sr < M ? i0 + sr : 0) * K, *br = B + (j0 + sr < N ? j0 + sr : 0) * K;
+    const bool aon = i0 + sr < M, bon = j0 + sr < N;
+    // no branches, and the values past M, N or K are zeroed only when the slice is stored, so the
+    // loads stay in flight under the previous slice's sums (VEC: K % 4 == 0 and rows 16-byte
+    // aligned, so a thread's 4 values are all in the row or all past K)
+    float va[GN_NQ][4], vb[GN_NQ][4];
+    auto fetch = [&](const float *row, int64_t k0, float (&v)[GN_NQ][4]) {
+#pragma unroll
+        for (int q = 0; q < GN_NQ; q++) {
+            const int64_t k = k0 + 32 * q + sk;
+            if (VEC) {
+                const float4 f = *(const float4 *)(row + (k < K ? k : 0));
+                v[q][0] = f.x, v[q][1] = f.y, v[q][2] = f.z, v[q][3] = f.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[q][j] = row[k + j < K ? k + j : K - 1];
+            }
         }
+    };
+    float c00 = 0.0f, c01 = 0.0f, c10 = 0.0f, c11 = 0.0f;
+    float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
+    fetch(ar, 0, va);
+    fetch(br, 0, vb);
+    for (int64_t k0 = 0; k0 < K; k0 += GN_KS) {
+        __syncthreads();  // the previous slice is consumed
+#pragma unroll
+        for (int q = 0; q < GN_NQ; q++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool in = k0 + 32 * q + sk + j < K;
+                As[32 * q + sk + j][sr] = aon && in ? va[q][j] : 0.0f;
+                Bs[32 * q + sk + j][sr] = bon && in ? vb[q][j] : 0.0f;
+            }
         __syncthreads();
-        float acc = 0.0f;
-        for (int k = 0; k < kc; k++) acc = acc + As[ty][k] * Bs[tx][k];
-        c = c + acc;
-        __syncthreads();
+        if (k0 + GN_KS < K) {  // uniform: the next slice's loads under this slice's sums
+            fetch(ar, k0 + GN_KS, va);
+            fetch(br, k0 + GN_KS, vb);
+        }
+        const int kn = K - k0 < GN_KS ? (int)(K - k0) : GN_KS;
+        if (kn == GN_KS) {
+            // groups of 8 k from two register sets: group g+1's reads go out before group g's
+            // sums (held there by the scheduling barriers)
+            float2 xa[2][8], xb[2][8];
+            auto rd = [&](int g, float2(&da)[8], float2(&db)[8]) {
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    da[q] = *(const float2 *)&As[8 * g + q][2 * r];
+                    db[q] = *(const float2 *)&Bs[8 * g + q][2 * c];
+                }
+            };
+            auto sum = [&](const float2(&da)[8], const float2(&db)[8]) {
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    s00 = s00 + da[q].x * db[q].x;
+                    s01 = s01 + da[q].x * db[q].y;
+                    s10 = s10 + da[q].y * db[q].x;
+                    s11 = s11 + da[q].y * db[q].y;
+                }
+            };
+            rd(0, xa[0], xb[0]);
+#pragma unroll
+            for (int g = 0; g < GN_KS / 8; g++) {
+                if (g + 1 < GN_KS / 8) rd(g + 1, xa[(g + 1) & 1], xb[(g + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                sum(xa[g & 1], xb[g & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            for (int k = 0; k < kn; k++) {
+                const float2 a2 = *(const float2 *)&As[k][2 * r], b2 = *(const float2 *)&Bs[k][2 * c];
+                s00 = s00 + a2.x * b2.x;
+                s01 = s01 + a2.x * b2.y;
+                s10 = s10 + a2.y * b2.x;
+                s11 = s11 + a2.y * b2.y;
+            }
+        }
+        if ((k0 + GN_KS) % QMH_GEMM_KC == 0 || k0 + GN_KS >= K) {  // a panel ends: C += its sums
+            c00 = c00 + s00, c01 = c01 + s01, c10 = c10 + s10, c11 = c11 + s11;
+            s00 = s01 = s10 = s11 = 0.0f;
+        }
     }
-    if (i < M && j < N) C[i * N + j] = c;
+    const int64_t i = i0 + 2 * r, j = j0 + 2 * c;
+    if (i < M && j < N) C[i * N + j] = c00;
+    if (i < M && j + 1 < N) C[i * N + j + 1] = c01;
+    if (i + 1 < M && j < N) C[(i + 1) * N + j] = c10;
+    if (i + 1 < M && j + 1 < N) C[(i + 1) * N + j + 1] = c11;
 }
 
 extern "C" int qmh_launch_gemm_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
                                   void *stream) {
     if (M <= 0 || N <= 0) return 0;
-    dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-    hipLaunchKernelGGL(k_gemm_nt, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);
+    if (K <= 0) return (int)hipMemsetAsync(C, 0, sizeof(float) * (size_t)M * (size_t)N, (hipStream_t)stream);
+    dim3 grid((unsigned)((N + GN_T - 1) / GN_T), (unsigned)((M + GN_T - 1) / GN_T));
+    if ((K & 3) == 0 && (((uintptr_t)A | (uintptr_t)B) & 15) == 0)
+        hipLaunchKernelGGL(k_gemm_nt<true>, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);
+    else
+        hipLaunchKernelGGL(k_gemm_nt<false>, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);
     return (int)hipGetLastError();
 }
 
