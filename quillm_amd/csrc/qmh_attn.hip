@@ -359,20 +359,8 @@ __device__ __forceinline__ void pv_mha_long(const float *__restrict__ s0, const 
     auto piece = [&](int j, int r) {  // r = j % (LA + 1)
         vload(j + LA < npc ? j + LA : npc - 1, vr[(r + LA) % (LA + 1)]);
         stage(j + 1, vr[(r + 1) % (LA + 1)], (j + 1) & 1);
-        if (chain) {
-            // out = out + p_t*v_t in t order; the piece's terms read at once, then added
-            const float4 *v4 = (const float4 *)(Vs2 + (size_t)(j & 1) * QMH_PV_CW * VS + (size_t)tid * VS);
-            float4 vc[PC / 4];
-#pragma unroll
-            for (int q = 0; q < PC / 4; q++) vc[q] = v4[q];
-#pragma unroll
-            for (int q = 0; q < PC / 4; q++) {
-                acc = acc + vc[q].x;
-                acc = acc + vc[q].y;
-                acc = acc + vc[q].z;
-                acc = acc + vc[q].w;
-            }
-        }
+        if (chain)  // out = out + p_t*v_t in t order (zeros staged past n change nothing)
+            acc = qmh_chain_lds(Vs2 + (size_t)(j & 1) * QMH_PV_CW * VS + (size_t)tid * VS, PC, acc);
         __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
     int j0 = 0;
@@ -558,9 +546,8 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
 // pv_short for the one-launch kernel: the same statistics, products and sums, with the products of
 // every position staged at once (Vs holds the whole context; this thread's exponentials read from
 // LDS together, then its 4*L4 products stored), one barrier, and the chain lanes (the first 16
-// threads) adding without further barriers, reading the next 32 positions' products while they add
-// the current ones. The chains stop at the last 32-position step holding a position below n (the
-// staged zeros past n change nothing: the sums start at +0 and are never -0).
+// threads) adding the n products of their column in order without further barriers
+// (qmh_chain_lds: float4 reads two sets of 32 ahead of the adds).
 template <int TC>
 __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1) / QMH_WG],
                                               float4 (&vv)[TC * QMH_PV_CW / 4 / QMH_WG], uint64_t etv,
@@ -639,29 +626,8 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
         dst[3 * VS] = on ? p * v.w : 0.0f;
     }
     __syncthreads();
-    if (tid < QMH_PV_CW) {
-        // out = out + p_t*v_t in t order, 32 positions per step
-        const float4 *v4 = (const float4 *)(Vs + (size_t)tid * VS);
-        const int nst = (n + 31) >> 5;
-        float acc = 0.0f;
-        float4 cur[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) cur[q] = v4[q];
-        for (int st = 0; st < nst; st++) {
-            float4 nxt[8];
-            const int sn = st + 1 < nst ? st + 1 : st;  // the last step re-reads itself
-#pragma unroll
-            for (int q = 0; q < 8; q++) nxt[q] = v4[8 * sn + q];
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                acc = acc + cur[q].x;
-                acc = acc + cur[q].y;
-                acc = acc + cur[q].z;
-                acc = acc + cur[q].w;
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q++) cur[q] = nxt[q];
-        }
+    if (tid < QMH_PV_CW) {  // out = out + p_t*v_t in t order
+        const float acc = qmh_chain_lds(Vs + (size_t)tid * VS, n, 0.0f);
         if (i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
     }
 }

@@ -390,8 +390,8 @@ struct ImageRegs {
 //   * the terms in LDS row-contiguous (each row's nb terms in block order, rows padded to
 //     mv_term_stride floats): a lane's term stores advance by a fixed block step (its row never
 //     changes), and after the last chunk every row's serial chain reads its terms as float4s
-//     (on MI355X a dependent add fed by 16-byte reads two sets ahead takes ~6.4 clocks, by a
-//     4-byte read per term ~12; W2's 344-term chains went 9.18 -> 8.24 us), then the epilogue.
+//     (qmh_chain_lds; W2's 344-term chains went 9.18 -> 8.24 us against 4-byte reads at stride
+//     R), then the epilogue.
 // Each workgroup quantizes the activation once for all of its rows.
 constexpr int MV_REC = 48;  // LDS bytes per activation record
 
@@ -416,61 +416,6 @@ typedef unsigned int mv_u32x4 __attribute__((ext_vector_type(4)));
 // stream does not evict the code, the activations and the norm gains from L2 (timed on MI355X:
 // 585 -> 591 tok/s at c5a)
 #define MV_NT 2
-
-// one row's serial chain over its nb contiguous terms (16-byte aligned): y = +0; y = y + t_b in
-// block order. Sets of 32 terms are read as 8 float4s into three register sets, two sets ahead of
-// the adds (the scheduling barriers hold the reads there): a dependent add fed this way takes ~6.4
-// clocks on MI355X, against ~12 with a 4-byte read per term.
-__device__ __forceinline__ float mv_chain(const float *tp, int nb) {
-    const float4 *p4 = (const float4 *)tp;
-    const int ns = nb >> 5;  // whole sets
-    float y = 0.0f;
-    float4 A[8], B[8], Cs[8];
-    auto rd = [&](float4(&d)[8], int st) {
-        st = st < ns ? st : ns - 1;  // past the last set: re-read it (no branch)
-#pragma unroll
-        for (int q = 0; q < 8; q++) d[q] = p4[8 * st + q];
-    };
-    auto add = [&](const float4(&d)[8]) {
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            y = y + d[q].x;
-            y = y + d[q].y;
-            y = y + d[q].z;
-            y = y + d[q].w;
-        }
-    };
-    if (ns > 0) {
-        rd(A, 0);
-        rd(B, 1);
-        int st = 0;
-        for (; st + 3 <= ns; st += 3) {
-            rd(Cs, st + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            add(A);
-            __builtin_amdgcn_sched_barrier(0);
-            rd(A, st + 3);
-            __builtin_amdgcn_sched_barrier(0);
-            add(B);
-            __builtin_amdgcn_sched_barrier(0);
-            rd(B, st + 4);
-            __builtin_amdgcn_sched_barrier(0);
-            add(Cs);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (st < ns) add(A);
-        if (st + 1 < ns) add(B);
-    }
-    for (int i = 8 * ns; i < (nb >> 2); i++) {
-        const float4 v = p4[i];
-        y = y + v.x;
-        y = y + v.y;
-        y = y + v.z;
-        y = y + v.w;
-    }
-    for (int b = nb & ~3; b < nb; b++) y = y + tp[b];
-    return y;
-}
 
 // One instance per weight type serves every matvec of the token (tile height R and activation
 // mode are uniform runtime values): the decode step's kernels then share one copy of this code in
@@ -663,7 +608,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
         const bool mine = i < rows_w;
         if (i0 > 0 && mine) ein = epi_fetch(a, row, pos);
         float y = 0.0f;
-        if (mine) y = mv_chain(T + (size_t)(tl * R + r) * SP, nb);
+        if (mine) y = qmh_chain_lds(T + (size_t)(tl * R + r) * SP, nb, 0.0f);
         mv_epilogue(a, mine ? row : a.rows, y, r, R >> 1, pos, ein, etab);
     }
 }
