@@ -1,7 +1,8 @@
 """The reference's own CLI and bench on the device path (oracle/hip_integration.patch):
 `quillm run --isa hip` (and QUILLM_ISA=hip) prints exactly the text `--isa scalar` prints, greedy and
-sampled, and `QUILLM_ISA=hip quillm-bench` completes its decode loop with a hip column -- the
-reference's cross-ISA identity check (tests/test_cli.sh:14-19) with hip added."""
+sampled, and `QUILLM_ISA=hip quillm-bench` completes its decode loop with a hip column and prints
+device GFLOP/s for its matvec and gemm kernel rows -- the reference's cross-ISA identity check
+(tests/test_cli.sh:14-19) with hip added."""
 import os
 import re
 import subprocess
@@ -59,3 +60,10 @@ def test_bench_hip_decode_loop(c2_model):
     for row in rows:
         m = re.search(r" hip\s+([0-9.]+)", row)
         assert m and float(m.group(1)) > 0, row
+    # the kernel rows' hip column: device time per qmh_matvec / qmh_matmul_nt call
+    kern = [line for line in r.stdout.splitlines() if line.startswith(("matvec", "gemm"))]
+    assert len(kern) == 8, r.stdout
+    for line in kern:
+        assert float(line.split()[-1]) > 0, line
+    dot = [line for line in r.stdout.splitlines() if line.startswith("dot f32")]
+    assert dot and dot[0].split()[-1] == "n/a", r.stdout
