@@ -329,12 +329,13 @@ def test_fused_slices_cover_every_position():
 
 def af_grid_map(nh, hd):
     """k_attn_fused's one-dimensional grid: 8 * ceil(nh/8) * (hd/16) workgroups; workgroup L takes
-    head (L % 8) + 8 * ((L / 8) / ncg), column group (L / 8) % ncg, and returns when the head is past
-    nh. (h, cg) of each workgroup, -1 for the ones that return."""
+    head (L % 8) * ceil(nh/8) + (L / 8) / ncg, column group (L / 8) % ncg, and returns when the head
+    is past nh. (h, cg) of each workgroup, -1 for the ones that return."""
     ncg = hd // CW
-    G = 8 * ((nh + 7) // 8) * ncg
+    hpx = (nh + 7) // 8
+    G = 8 * hpx * ncg
     L = np.arange(G)
-    h = (L & 7) + 8 * ((L >> 3) // ncg)
+    h = (L & 7) * hpx + (L >> 3) // ncg
     cg = (L >> 3) % ncg
     return L, np.where(h < nh, h, -1), np.where(h < nh, cg, -1)
 
@@ -343,13 +344,24 @@ def af_grid_map(nh, hd):
 @pytest.mark.parametrize("hd", [48, 64, 128])
 def test_fused_grid_places_each_head_on_one_xcd(nh, hd):
     """Every (head, column group) has exactly one workgroup, and a head's workgroups have one
-    dispatch slot modulo 8 (the XCD the round-robin dispatcher gives them)."""
+    dispatch slot modulo 8 (the XCD the round-robin dispatcher gives them). The heads of one XCD
+    are consecutive, so the query heads that share a kv head share as few XCDs as possible:
+    ceil(group / heads per XCD) + 1 at most."""
     L, h, cg = af_grid_map(nh, hd)
     live = h >= 0
     pairs = h[live] * (hd // CW) + cg[live]
     assert np.array_equal(np.sort(pairs), np.arange(nh * (hd // CW)))
     for head in range(nh):
         assert len(set((L[h == head] % 8).tolist())) == 1
+    hpx = (nh + 7) // 8
+    for x in range(8):
+        hs = sorted(set(h[live & (L % 8 == x)].tolist()))
+        assert hs == list(range(x * hpx, x * hpx + len(hs)))
+    for group in (1, 2, 4, 8):
+        if nh % group == 0:
+            for kvh in range(nh // group):
+                xcds = set((L[live & (h // group == kvh)] % 8).tolist())
+                assert len(xcds) <= -(-group // hpx) + 1
 
 
 def test_model_catches_an_out_of_range_clamp():
