@@ -515,13 +515,18 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
         attn_pv_chunks<TC, true>(att, V, out, n, n_heads, n_heads, hd, max_seq);
         return;
     }
+    // grouped heads, n_heads % 8 == 0: workgroups x, x + 8, ... (one XCD: x % 8 of the linear id,
+    // gridDim.x being n_heads) take consecutive heads, so a group's query heads read their kv head's
+    // V through one or two L2s
+    const int bx = (int)blockIdx.x;
+    const int h = n_kv != n_heads && (n_heads & 7) == 0 ? (bx & 7) * (n_heads >> 3) + (bx >> 3) : bx;
     if (n > TC) {
-        pv_mha_long<3>(att + (size_t)blockIdx.x * max_seq, V, out, n, blockIdx.x, blockIdx.x / (n_heads / n_kv),
-                       blockIdx.y * QMH_PV_CW, hd, hd * n_kv, pv_smem, pv_smem + QMH_PV_LONG);
+        pv_mha_long<3>(att + (size_t)h * max_seq, V, out, n, h, h / (n_heads / n_kv), blockIdx.y * QMH_PV_CW, hd,
+                       hd * n_kv, pv_smem, pv_smem + QMH_PV_LONG);
         return;
     }
     const int tid = threadIdx.x;
-    const int h = blockIdx.x, kvh = h / (n_heads / n_kv), i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
+    const int kvh = h / (n_heads / n_kv), i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
     const float *s0 = att + (size_t)h * max_seq;
     // loads: expf's table (oldest, so storing it to LDS below waits for nothing else), the head's
     // scores, then the V float4s (position k*64 + tid/4, columns c .. c+3; columns past hd
