@@ -390,10 +390,20 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const float *__restrict__ A, co
     if (i + 1 < M && j + 1 < N) C[(i + 1) * N + j + 1] = c11;
 }
 
+// C = 0 for K = 0 (the reference's zeroing with no panel to add), as a kernel: no memset node if the
+// caller records the call into a graph
+__global__ void k_gemm_zero(float *C, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        C[i] = 0.0f;
+}
+
 extern "C" int qmh_launch_gemm_nt(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
                                   void *stream) {
     if (M <= 0 || N <= 0) return 0;
-    if (K <= 0) return (int)hipMemsetAsync(C, 0, sizeof(float) * (size_t)M * (size_t)N, (hipStream_t)stream);
+    if (K <= 0) {
+        hipLaunchKernelGGL(k_gemm_zero, dim3(grid_for(M * N)), dim3(256), 0, (hipStream_t)stream, C, M * N);
+        return (int)hipGetLastError();
+    }
     dim3 grid((unsigned)((N + GN_T - 1) / GN_T), (unsigned)((M + GN_T - 1) / GN_T));
     if ((K & 3) == 0 && (((uintptr_t)A | (uintptr_t)B) & 15) == 0)
         hipLaunchKernelGGL(k_gemm_nt<true>, grid, dim3(256), 0, (hipStream_t)stream, A, B, C, M, N, K);

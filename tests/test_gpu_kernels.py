@@ -142,6 +142,17 @@ def test_gemm_nt(gpu, oracle):
         assert np.array_equal(bits(got), bits(oracle.gemm_nt(A, B))), (M, N, K)
 
 
+def test_gemm_nt_empty_k(gpu):
+    """K = 0: the reference zeroes C and has no panel to add (src/gemm_driver.h:9-10)."""
+    L = gpu.load_library()
+    M, N = 37, 70
+    dA, dB = gpu.DeviceBuffer(4), gpu.DeviceBuffer(4)
+    dC = dev(gpu, np.full(M * N, 7.0, np.float32))
+    gpu._check(L.qmh_matmul_nt(dA.ptr, dB.ptr, dC.ptr, M, N, 0, None), "gemm")
+    gpu.sync()
+    assert np.array_equal(bits(dC.to_array(np.float32)), np.zeros(M * N, np.uint32))
+
+
 @pytest.mark.parametrize("n", [1, 7, 77, 288, 4096, 11008])
 def test_elementwise(gpu, oracle, n):
     L = gpu.load_library()
