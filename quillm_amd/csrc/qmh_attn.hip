@@ -639,7 +639,9 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 
 // ============================================================================ one launch per step
 
-// The decode step's whole attention in one launch, for contexts of up to QMH_AF_TC positions:
+// The decode step's whole attention in one launch, for contexts of up to TC positions (two
+// instances: TC = 640 for head_dim 48, 64 and 128; TC = 1024 for head_dim 64 and 128, whose slices
+// of at most 256 positions keep one chain lane per position):
 // workgroup (cg, h) owns query head h's output columns 16*cg .. +15 (as k_attn_pv_mha) and
 // computes the scores of a slice of the head's positions,
 // [cg*sp, cg*sp + sp) with sp = ceil(n / (head_dim/16)) rounded up to 4. Its K slice arrives as
@@ -665,17 +667,18 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 // writes, so that a test can run the bounded wait to its end from the host. The host launches at
 // most as many workgroups as the device holds at once.
 #define QMH_AF_TC 640
+#define QMH_AF_TC2 1024
 #define QMH_AF_SPIN (1u << 16)
 // workgroups of k_attn_fused's grid: 8 XCDs x ceil(n_heads / 8) heads x head_dim/16
 __host__ __device__ __forceinline__ int af_grid(int n_heads, int hd) { return 8 * ((n_heads + 7) / 8) * (hd / QMH_PV_CW); }
 
-template <int HD>
+template <int HD, int TC>
 __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ Kt,
                                                        const float *__restrict__ V, float *__restrict__ out,
                                                        uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync,
                                                        int n_heads, int n_kv, int max_seq, float scale, int layer,
                                                        int n_layers, uint32_t spin, uint32_t skew) {
-    constexpr int TC = QMH_AF_TC, CW = QMH_PV_CW, NCG = HD / CW;
+    constexpr int CW = QMH_PV_CW, NCG = HD / CW;
     constexpr int SPM = ((TC + NCG - 1) / NCG + 3) / 4 * 4;          // most positions of one slice
     constexpr int KS = HD + 4;                                       // LDS row stride of the K slice
     constexpr int KL4 = (SPM / 4 * HD + QMH_WG - 1) / QMH_WG;        // float4 K loads per thread
@@ -801,50 +804,70 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
     pv_short_flow<TC>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
 }
 
-// dynamic LDS bytes of k_attn_fused<HD>: the larger of the K slice and the V sum's buffers
-static size_t af_lds_bytes(int hd) {
-    const int ncg = hd / QMH_PV_CW, spm = ((QMH_AF_TC + ncg - 1) / ncg + 3) / 4 * 4;
-    const size_t kslice = (size_t)spm * (hd + 4), pv = (size_t)QMH_AF_TC + QMH_PV_CW * (QMH_AF_TC + 4);
+// dynamic LDS bytes of k_attn_fused<HD, TC>: the larger of the K slice and the V sum's buffers
+static size_t af_lds_bytes(int hd, int tc) {
+    const int ncg = hd / QMH_PV_CW, spm = ((tc + ncg - 1) / ncg + 3) / 4 * 4;
+    const size_t kslice = (size_t)spm * (hd + 4), pv = (size_t)tc + QMH_PV_CW * (size_t)(tc + 4);
     return sizeof(float) * (kslice > pv ? kslice : pv);
 }
 
-extern "C" int qmh_attn_fused_max_n(void) { return QMH_AF_TC; }
+extern "C" int qmh_attn_fused_max_n(int instance) { return instance == 0 ? QMH_AF_TC : instance == 1 ? QMH_AF_TC2 : 0; }
 
-// 1 when k_attn_fused takes the shape: head_dim 48, 64 or 128, max_seq a whole number of float4s, and
-// no more workgroups than the device holds at once (every head's workgroups run together); else 0
-extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
-    if ((head_dim != 128 && head_dim != 64 && head_dim != 48) || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 ||
-        n_heads % n_kv_heads)
-        return 0;
-    int dev = 0, ncu = 0, per = 0;
-    const void *k = head_dim == 128 ? (const void *)k_attn_fused<128>
-                    : head_dim == 64 ? (const void *)k_attn_fused<64> : (const void *)k_attn_fused<48>;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, QMH_WG, af_lds_bytes(head_dim)) != hipSuccess)
-        return 0;
-    return (long long)af_grid(n_heads, head_dim) <= (long long)per * ncu;
+// the kernel of an instance for a head size, or NULL
+static const void *af_kernel(int head_dim, int instance) {
+    if (instance == 0)
+        return head_dim == 128 ? (const void *)k_attn_fused<128, QMH_AF_TC>
+               : head_dim == 64 ? (const void *)k_attn_fused<64, QMH_AF_TC>
+               : head_dim == 48 ? (const void *)k_attn_fused<48, QMH_AF_TC> : NULL;
+    if (instance == 1)
+        return head_dim == 128 ? (const void *)k_attn_fused<128, QMH_AF_TC2>
+               : head_dim == 64 ? (const void *)k_attn_fused<64, QMH_AF_TC2> : NULL;
+    return NULL;
 }
 
-// the caller has checked qmh_attn_fused_supported for the shape; stall != 0 (tests only): the
-// readers wait for an epoch nobody writes, for 64 polls
+// the number of instances k_attn_fused takes the shape with (0, 1: contexts up to 640, 2: also up to
+// 1024): head_dim 48, 64 or 128 (the second instance: 64 or 128), max_seq a whole number of float4s,
+// and no more workgroups than the device holds at once (every head's workgroups run together)
+extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
+    if (max_seq % 4 || max_seq < 4 || n_kv_heads < 1 || n_heads % n_kv_heads || !af_kernel(head_dim, 0)) return 0;
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    int count = 0;
+    for (int i = 0; i < 2; i++) {
+        int per = 0;
+        const void *k = af_kernel(head_dim, i);
+        if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, QMH_WG, af_lds_bytes(head_dim, qmh_attn_fused_max_n(i))) !=
+                      hipSuccess ||
+            (long long)af_grid(n_heads, head_dim) > (long long)per * ncu)
+            break;
+        count = i + 1;
+    }
+    return count;
+}
+
+// the caller has checked qmh_attn_fused_supported for the shape and instance; stall != 0 (tests
+// only): the readers wait for an epoch nobody writes, for 64 polls
 extern "C" int qmh_launch_attn_fused(const float *q, const float *kcache, const float *vcache, float *out,
                                      uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync, int n_heads,
                                      int n_kv_heads, int head_dim, int max_seq, float scale, int layer, int n_layers,
-                                     int stall, void *stream) {
-    if ((head_dim != 128 && head_dim != 64 && head_dim != 48) || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 ||
-        n_heads % n_kv_heads)
-        return (int)hipErrorNotSupported;
+                                     int instance, int stall, void *stream) {
+    const void *k = af_kernel(head_dim, instance);
+    if (!k || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 || n_heads % n_kv_heads) return (int)hipErrorNotSupported;
     const dim3 grid(af_grid(n_heads, head_dim));
-    const size_t lds = af_lds_bytes(head_dim);
+    const size_t lds = af_lds_bytes(head_dim, qmh_attn_fused_max_n(instance));
     hipStream_t s = (hipStream_t)stream;
     const uint32_t spin = stall ? 64u : QMH_AF_SPIN, skew = stall ? 1u : 0u;
-#define QMH_AF(HD)                                                                                             \
-    hipLaunchKernelGGL(k_attn_fused<HD>, grid, dim3(QMH_WG), lds, s, q, kcache, vcache, out, attp, pos_ptr, sync, \
-                       n_heads, n_kv_heads, max_seq, scale, layer, n_layers, spin, skew)
-    if (head_dim == 128) QMH_AF(128);
-    else if (head_dim == 64) QMH_AF(64);
-    else QMH_AF(48);
+#define QMH_AF(HD, TC)                                                                                            \
+    hipLaunchKernelGGL((k_attn_fused<HD, TC>), grid, dim3(QMH_WG), lds, s, q, kcache, vcache, out, attp, pos_ptr, \
+                       sync, n_heads, n_kv_heads, max_seq, scale, layer, n_layers, spin, skew)
+    if (instance == 1) {
+        if (head_dim == 128) QMH_AF(128, QMH_AF_TC2);
+        else QMH_AF(64, QMH_AF_TC2);
+    } else if (head_dim == 128) QMH_AF(128, QMH_AF_TC);
+    else if (head_dim == 64) QMH_AF(64, QMH_AF_TC);
+    else QMH_AF(48, QMH_AF_TC);
 #undef QMH_AF
     return (int)hipGetLastError();
 }

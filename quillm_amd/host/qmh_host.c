@@ -390,11 +390,12 @@ struct qmh_model {
     float *h_logits;   /* pinned [vocab] */
     hipGraph_t graph_fwd, graph_greedy;
     hipGraphExec_t exec_fwd, exec_greedy;
-    /* the same steps with the attention in one launch (k_attn_fused), for positions below
-     * qmh_attn_fused_max_n() when af_ok */
-    hipGraph_t graph_fwd_af, graph_greedy_af;
-    hipGraphExec_t exec_fwd_af, exec_greedy_af;
-    int af_ok;
+    /* the same steps with the attention in one launch (k_attn_fused), instance i for positions
+     * below qmh_attn_fused_max_n(i), i < af_n */
+    hipGraph_t graph_fwd_af[2], graph_greedy_af[2];
+    hipGraphExec_t exec_fwd_af[2], exec_greedy_af[2];
+    int af_n;          /* k_attn_fused's instances that take the model's shape (0: none) */
+    int af_inst;       /* the instance ST_ATTN launches */
     int af_stall;      /* QMH_AF_FORCE_STALL (tests): the one-launch attention's waits run out */
     uint64_t *d_attp;  /* [n_heads][max_seq] epoch-tagged scores of k_attn_fused */
     uint32_t *d_sync;  /* [0] decode steps (k_embed), [1] k_attn_fused's wait status */
@@ -443,9 +444,10 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     case ST_PV: /* src/model.c:147-154 */
         return qmh_launch_attn_pv(m->d_att, vl, m->d_xb, pos_ptr, c->n_heads, c->n_kv_heads, m->hd, S_, s);
     case ST_ATTN: /* src/model.c:137-156 in one launch */
-        if (!m->af_ok) return (int)hipErrorNotSupported;
+        if (m->af_inst >= m->af_n) return (int)hipErrorNotSupported;
         return qmh_launch_attn_fused(m->d_q, kl, vl, m->d_xb, m->d_attp, pos_ptr, m->d_sync, c->n_heads, c->n_kv_heads,
-                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), l, c->n_layers, m->af_stall, s);
+                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), l, c->n_layers, m->af_inst, m->af_stall,
+                                     s);
     case ST_WO: /* x += Wo xb (src/model.c:178-179) */
         mv_args_for(&L->wo, &a);
         a.x = m->d_xb;
@@ -494,9 +496,11 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     return (int)hipErrorInvalidValue;
 }
 
-/* af: the attention in one launch (the step's position is below qmh_attn_fused_max_n()) */
+/* af: 0, or the attention in one launch by instance af - 1 (the step's position is below
+ * qmh_attn_fused_max_n(af - 1)) */
 static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax, int af) {
     const qmh_config *c = &m->cfg;
+    if (af) m->af_inst = af - 1;
     LCHK(qmh_launch_embed(m->d_embd, m->emb_dtype, c->dim, c->vocab_size, m->d_tokpos, m->d_x, m->d_sync, s));
     static const int order[6] = {ST_QKV, ST_SCORES, ST_PV, ST_WO, ST_W13, ST_W2};
     static const int order_af[5] = {ST_QKV, ST_ATTN, ST_WO, ST_W13, ST_W2};
@@ -512,13 +516,21 @@ static int enqueue_step(qmh_model *m, hipStream_t s, int with_argmax, int af) {
     return 0;
 }
 
+/* the attention of a step at position pos: 0 (two launches) or 1 + the one-launch instance */
+static int af_for(const qmh_model *m, int32_t pos) {
+    for (int i = 0; i < m->af_n; i++)
+        if (pos < qmh_attn_fused_max_n(i)) return i + 1;
+    return 0;
+}
+
 /* one decode step at position pos on the library stream: a graph replay, or the same launches one by
  * one */
 static hipError_t run_step(qmh_model *m, int with_argmax, int32_t pos) {
-    const int af = m->af_ok && pos < qmh_attn_fused_max_n();
-    if (m->use_graph)
-        return hipGraphLaunch(with_argmax ? (af ? m->exec_greedy_af : m->exec_greedy) : (af ? m->exec_fwd_af : m->exec_fwd),
-                              g_stream);
+    const int af = af_for(m, pos);
+    if (m->use_graph) {
+        if (af) return hipGraphLaunch(with_argmax ? m->exec_greedy_af[af - 1] : m->exec_fwd_af[af - 1], g_stream);
+        return hipGraphLaunch(with_argmax ? m->exec_greedy : m->exec_fwd, g_stream);
+    }
     return enqueue_step(m, g_stream, with_argmax, af) ? hipErrorLaunchFailure : hipSuccess;
 }
 
@@ -526,7 +538,7 @@ static hipError_t run_step(qmh_model *m, int with_argmax, int32_t pos) {
  * word cleared for the next). copied: the caller already copied d_sync[1] to h_sync before it
  * synchronized */
 static int check_attn_sync_copied(qmh_model *m, int copied) {
-    if (!m->af_ok) return 0;
+    if (!m->af_n) return 0;
     if (!copied) HIPCHK(hipMemcpy(m->h_sync, m->d_sync + 1, sizeof(uint32_t), hipMemcpyDeviceToHost));
     if (*m->h_sync == 0) return 0;
     const uint32_t st = *m->h_sync;
@@ -553,6 +565,11 @@ int qmh_model_time_stage(qmh_model *m, int which, int32_t pos, int iters, double
                          double *bytes_per_launch) {
     if (!m || which < 0 || which >= ST_COUNT || iters < 1 || pos < 0 || pos >= m->cfg.max_seq)
         return fail("time_stage: bad arguments");
+    if (which == ST_ATTN) {
+        const int af = af_for(m, pos);
+        if (!af) return fail("time_stage: no one-launch attention for position %d", (int)pos);
+        m->af_inst = af - 1;
+    }
     /* the stages read token and position from device memory: set both (a greedy run leaves
      * the position one past its last step) */
     int32_t *slot = m->h_tokpos;
@@ -694,10 +711,12 @@ void qmh_model_free(qmh_model *m) {
     if (m->exec_greedy) hipGraphExecDestroy(m->exec_greedy);
     if (m->graph_fwd) hipGraphDestroy(m->graph_fwd);
     if (m->graph_greedy) hipGraphDestroy(m->graph_greedy);
-    if (m->exec_fwd_af) hipGraphExecDestroy(m->exec_fwd_af);
-    if (m->exec_greedy_af) hipGraphExecDestroy(m->exec_greedy_af);
-    if (m->graph_fwd_af) hipGraphDestroy(m->graph_fwd_af);
-    if (m->graph_greedy_af) hipGraphDestroy(m->graph_greedy_af);
+    for (int i = 0; i < 2; i++) {
+        if (m->exec_fwd_af[i]) hipGraphExecDestroy(m->exec_fwd_af[i]);
+        if (m->exec_greedy_af[i]) hipGraphExecDestroy(m->exec_greedy_af[i]);
+        if (m->graph_fwd_af[i]) hipGraphDestroy(m->graph_fwd_af[i]);
+        if (m->graph_greedy_af[i]) hipGraphDestroy(m->graph_greedy_af[i]);
+    }
     if (m->layers) {
         for (int l = 0; l < m->cfg.n_layers; l++) {
             weight_release(&m->layers[l].qkv);
@@ -833,13 +852,13 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMemsetAsync(m->d_v, 0, kv_bytes, g_stream));
     HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
     /* the one-launch attention: its score words start at epoch 0, which no launch uses */
-    m->af_ok = getenv("QMH_NO_FUSED_ATTN") == NULL &&
-               qmh_attn_fused_supported(c->n_heads, c->n_kv_heads, m->hd, (int)S_);
+    m->af_n = getenv("QMH_NO_FUSED_ATTN") ? 0 : qmh_attn_fused_supported(c->n_heads, c->n_kv_heads, m->hd, (int)S_);
+    if (m->af_n > 1 && getenv("QMH_FUSED_ATTN_640")) m->af_n = 1;
     m->af_stall = getenv("QMH_AF_FORCE_STALL") != NULL;
     HIPCHK(hipMalloc((void **)&m->d_sync, sizeof(uint32_t) * 2));
     HIPCHK(hipMemsetAsync(m->d_sync, 0, sizeof(uint32_t) * 2, g_stream));
     HIPCHK(hipHostMalloc((void **)&m->h_sync, sizeof(uint32_t), hipHostMallocDefault));
-    if (m->af_ok) {
+    if (m->af_n) {
         HIPCHK(hipMalloc((void **)&m->d_attp, sizeof(uint64_t) * (size_t)c->n_heads * S_));
         HIPCHK(hipMemsetAsync(m->d_attp, 0, sizeof(uint64_t) * (size_t)c->n_heads * S_, g_stream));
     }
@@ -881,10 +900,13 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     m->use_graph = getenv("QMH_NO_GRAPH") == NULL;
     if (m->use_graph && capture(m, 0, 0, &m->graph_fwd, &m->exec_fwd)) return -1;
     if (m->use_graph && capture(m, 1, 0, &m->graph_greedy, &m->exec_greedy)) return -1;
-    if (m->use_graph && m->af_ok && capture(m, 0, 1, &m->graph_fwd_af, &m->exec_fwd_af)) return -1;
-    if (m->use_graph && m->af_ok && capture(m, 1, 1, &m->graph_greedy_af, &m->exec_greedy_af)) return -1;
+    for (int i = 0; i < m->af_n; i++) {
+        if (m->use_graph && capture(m, 0, i + 1, &m->graph_fwd_af[i], &m->exec_fwd_af[i])) return -1;
+        if (m->use_graph && capture(m, 1, i + 1, &m->graph_greedy_af[i], &m->exec_greedy_af[i])) return -1;
+    }
     if (!m->use_graph && enqueue_step(m, g_stream, 0, 0)) return -1; /* validate the launches once */
-    if (!m->use_graph && m->af_ok && enqueue_step(m, g_stream, 0, 1)) return -1;
+    for (int i = 0; i < m->af_n; i++)
+        if (!m->use_graph && enqueue_step(m, g_stream, 0, i + 1)) return -1;
     HIPCHK(hipStreamSynchronize(g_stream));
     return 0;
 }
@@ -987,7 +1009,7 @@ float *qmh_model_forward(qmh_model *m, int32_t token, int32_t pos) {
     if (e == hipSuccess)
         e = hipMemcpyAsync(m->h_logits, m->d_logits, sizeof(float) * (size_t)m->cfg.vocab_size, hipMemcpyDeviceToHost,
                            g_stream);
-    if (e == hipSuccess && m->af_ok)
+    if (e == hipSuccess && m->af_n)
         e = hipMemcpyAsync(m->h_sync, m->d_sync + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) {

@@ -17,8 +17,8 @@ passes. The formulas restate the kernels' own index arithmetic, line by line:
   * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:393-530: one workgroup per query head, float4 V
                           loads of its kv head clamped to position n-1 and column head_dim-4
   * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:532-555: kernel choice and dynamic LDS
-  * k_attn_fused<HD>      quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= 640): the
-                          K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
+  * k_attn_fused<HD,TC>   quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= TC, TC 640
+                          for head_dim 48/64/128 and 1024 for head_dim 64/128): the K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
                           score words, and that the slices of a head's workgroups cover its n
                           positions exactly once (a position nobody writes would leave its readers
                           waiting until their bounded wait runs out)
@@ -213,27 +213,34 @@ def pv_mha_long(nh, nkv, hd, S, n, ext, lds_floats):
 LDS_MAX = 160 * 1024 - 1024  # per workgroup on gfx950, less the kernels' static LDS
 
 AF_TC = 640
+AF_TC2 = 1024  # the second instance (head_dim 64 and 128)
 
 
-def af_lds_floats(hd):
+def af_instances(hd):
+    """The instances (their TC) qmh_attn_fused_supported can return for a head size."""
+    return [AF_TC, AF_TC2] if hd in (64, 128) else [AF_TC] if hd == 48 else []
+
+
+def af_lds_floats(hd, TC):
     ncg = hd // CW
-    spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
-    return max(spm * (hd + 4), AF_TC + CW * (AF_TC + 4))
+    spm = ((TC + ncg - 1) // ncg + 3) // 4 * 4
+    return max(spm * (hd + 4), TC + CW * (TC + 4))
 
 
-def fused(nh, nkv, hd, S, n, ext):
-    """k_attn_fused<HD> over its (head, column group) workgroups x 256 threads (the grid's placement:
-    af_grid_map), n <= 640 positions: every thread loads its
+def fused(nh, nkv, hd, S, n, ext, TC=AF_TC):
+    """k_attn_fused<HD,TC> over its (head, column group) workgroups x 256 threads (the grid's
+    placement: af_grid_map), n <= TC positions: every thread loads its
     part of the K slice and its V float4s (as k_attn_pv_mha), the threads below the slice's position
-    count run the score chains, every thread reads the head's scores, stages its products for all 640
+    count run the score chains, every thread reads the head's scores, stages its products for all TC
     positions, and the first 16 threads run the V sum's chains (pv_short_flow)."""
-    assert hd in (48, 64, 128) and S % 4 == 0 and S >= 4 and n <= min(AF_TC, S)
+    assert TC in af_instances(hd) and S % 4 == 0 and S >= 4 and n <= min(TC, S)
+    AF_TC = TC
     ncg, kvd = hd // CW, hd * nkv
     spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
     KS, KL4 = hd + 4, (spm // 4 * hd + WG - 1) // WG
     L4, SK, VS = AF_TC * CW // 4 // WG, (AF_TC + WG - 1) // WG, AF_TC + 4
     assert spm <= WG and L4 * (WG // 4) == AF_TC
-    lds = af_lds_floats(hd)
+    lds = af_lds_floats(hd, TC)
     assert 4 * lds <= LDS_MAX
     tid = np.arange(WG)
     inb("af q", np.arange(nh)[:, None] * hd + 4 * tid[tid < hd // 4][None, :] + 3, ext.q)
@@ -271,7 +278,7 @@ def fused(nh, nkv, hd, S, n, ext):
     t = tid[None, :] + WG * np.arange(SK)[:, None]
     inb("af poll", np.arange(nh)[:, None] * S + t[t < n][None, :], ext.att)
     inb("af P", t[t < n], AF_TC)
-    # staging: every thread, positions k*64 + tid/4 (all < 640), rows 4*(tid%4) + r of Vs
+    # staging: every thread, positions k*64 + tid/4 (all < TC), rows 4*(tid%4) + r of Vs
     ts = np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :]
     assert ts.max() < AF_TC
     inb("af P read", ts[ts < n], AF_TC)
@@ -313,18 +320,25 @@ def test_decode_attention_indices_in_bounds(shape):
     for pos in positions(S):
         scores(nh, nkv, hd, S, pos, ext)
         pv(nh, nkv, hd, S, pos, ext)
-        # the one-launch kernel: shapes qmh_attn_fused_supported takes, positions below 640
-        if hd in (48, 64, 128) and S % 4 == 0 and S >= 4 and pos + 1 <= AF_TC:
-            fused(nh, nkv, hd, S, pos + 1, ext)
+        # the one-launch kernel: shapes qmh_attn_fused_supported takes, each instance at the
+        # positions the host gives it (below 640: the first; 640..1023: the second) and the first
+        # at every position below 640
+        if S % 4 == 0 and S >= 4:
+            for TC in af_instances(hd):
+                if pos + 1 <= TC:
+                    fused(nh, nkv, hd, S, pos + 1, ext, TC)
 
 
-def test_fused_slices_cover_every_position():
-    """Every n in 1..640 and every head_dim the one-launch kernel takes: its workgroups' score slices
+@pytest.mark.parametrize("TC", [AF_TC, AF_TC2])
+def test_fused_slices_cover_every_position(TC):
+    """Every n in 1..TC and every head_dim the instance takes: its workgroups' score slices
     cover positions 0..n-1 once each (fused() asserts it), here with the other checks too."""
     for hd in (48, 64, 128):
-        ext = Extents(2, 1, hd, 640)
-        for n in range(1, AF_TC + 1):
-            fused(2, 1, hd, 640, n, ext)
+        if TC not in af_instances(hd):
+            continue
+        ext = Extents(2, 1, hd, TC)
+        for n in range(1, TC + 1):
+            fused(2, 1, hd, TC, n, ext, TC)
 
 
 def af_grid_map(nh, hd):

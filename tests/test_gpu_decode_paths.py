@@ -2,10 +2,11 @@
 
 * The one-launch attention (k_attn_fused: scores, softmax and V sum, the scores exchanged between a
   head's workgroups as epoch-tagged words) against the CPU oracle, at decode positions on both sides
-  of its 640-position limit, for the head shapes it takes (head_dim 128, 64 and 48; one and four
-  query heads per kv head).
-* The same steps replayed from hipGraphs, enqueued kernel by kernel (QMH_NO_GRAPH), and with the
-  two-launch attention (QMH_NO_FUSED_ATTN): identical logits and greedy ids.
+  of its instances' limits (640 positions; 1024 for head_dim 64 and 128), for the head shapes it
+  takes (head_dim 128, 64 and 48; one and four query heads per kv head).
+* The same steps replayed from hipGraphs, enqueued kernel by kernel (QMH_NO_GRAPH), with the
+  two-launch attention (QMH_NO_FUSED_ATTN) and with the 640-position instance alone
+  (QMH_FUSED_ATTN_640): identical logits and greedy ids.
 * A rerun of the same decode steps gives the same bits (reference: tests/test_model.c:84-94 reruns a
   model, tests/test_threads.c:56-94 compares thread counts bitwise).
 * The bounded wait of the one-launch attention, run to its end from the host (QMH_AF_FORCE_STALL):
@@ -21,14 +22,16 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-# dim / n_heads = 128, 64 (4 query heads on one kv head) and 48; contexts past 640 for the first two
+# dim / n_heads = 128, 64 (4 query heads on one kv head) and 48; contexts past 640 for the first two,
+# past 1024 for af64x
 AF_SHAPES = {
     "af128": dict(dim=256, hidden_dim=384, n_layers=2, n_heads=2, n_kv_heads=2, vocab_size=300, max_seq=700),
     "af64g": dict(dim=256, hidden_dim=384, n_layers=2, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=664),
     "af48": dict(dim=96, hidden_dim=160, n_layers=2, n_heads=2, n_kv_heads=1, vocab_size=300, max_seq=100),
+    "af64x": dict(dim=256, hidden_dim=384, n_layers=2, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=1040),
 }
-# prompt length and decode steps: the steps cross position 640 where the context allows it
-RUN = {"af128": (630, 20), "af64g": (632, 20), "af48": (60, 30)}
+# prompt length and decode steps: the steps cross position 640 (and 1024) where the context allows it
+RUN = {"af128": (630, 20), "af64g": (632, 20), "af48": (60, 30), "af64x": (1014, 20)}
 
 
 def bits(a):
@@ -119,7 +122,7 @@ def test_fused_attention_from_position_zero(gpu, oracle, af_models):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("shape", ["af128", "af64g"])
+@pytest.mark.parametrize("shape", ["af128", "af64g", "af64x"])
 def test_decode_variants_agree(gpu, af_models, shape):
     path = af_models[(shape, "q4_0")]
     P, G = RUN[shape]
@@ -127,6 +130,7 @@ def test_decode_variants_agree(gpu, af_models, shape):
     runs = {}
     for name, kv in [("graph+fused", {}), ("no graph", {"QMH_NO_GRAPH": "1"}),
                      ("two-launch attention", {"QMH_NO_FUSED_ATTN": "1"}),
+                     ("640-position instance alone", {"QMH_FUSED_ATTN_640": "1"}),
                      ("no graph, two-launch", {"QMH_NO_GRAPH": "1", "QMH_NO_FUSED_ATTN": "1"})]:
         say(f"case {shape}: {name}")
         runs[name] = decode(gpu, path, prompt, G, **kv)
@@ -156,17 +160,20 @@ def test_decode_rerun_is_bitwise_deterministic(gpu, af_models):
 
 def test_fused_attention_wait_runs_out(gpu, af_models):
     """QMH_AF_FORCE_STALL makes every workgroup wait for an epoch nobody writes: the wait ends after
-    its bound, the kernels finish, and the library reports the failure (forward returns None). A
-    position past the one-launch kernel's limit takes the two-launch attention, which does not wait."""
-    path = af_models[("af128", "q4_0")]
+    its bound, the kernels finish, and the library reports the failure (forward returns None), for
+    both instances. A position past the one-launch kernel's limit takes the two-launch attention,
+    which does not wait."""
+    path = af_models[("af64x", "q4_0")]
     with env(QMH_AF_FORCE_STALL="1"):
         m = gpu.Model.load(path)
     with m:
-        assert m.forward(5, 650) is not None
+        assert m.forward(5, 1030) is not None
         assert m.forward(5, 3) is None
         assert "ran out" in gpu.last_error()
+        assert m.forward(5, 700) is None
+        assert "ran out" in gpu.last_error()
         # the status word was cleared with the report: the next long-context step succeeds
-        assert m.forward(5, 651) is not None
+        assert m.forward(5, 1031) is not None
 
 
 def test_fused_attention_stage_timer(gpu, oracle, af_models):
@@ -177,7 +184,7 @@ def test_fused_attention_stage_timer(gpu, oracle, af_models):
     want, want_ids = oracle.run_model(path, prompt, n_gen=4)
     with gpu.Model.load(path) as m:
         m.prefill(prompt, 0)
-        for pos in (0, 39, 600, 639):
+        for pos in (0, 39, 600, 639, 640, 663):
             ms, nbytes = m.time_stage("attn", 9, pos=pos)
             assert ms > 0 and nbytes == 0
         m.prefill(prompt, 0)  # the timer wrote the caches at its positions

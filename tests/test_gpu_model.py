@@ -239,9 +239,14 @@ def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
 
 @pytest.mark.parametrize("name,dims,wt,spans", [
     # one query head per kv head, head_dim 128: decode attention past one 640-position chunk
-    # (positions 638-642 cross into the second chunk, 1279-1281 into the third)
+    # (positions 638-642 cross into the second chunk, 1279-1281 into the third), and across the
+    # one-launch attention's instances (640 and 1024 positions)
     ("mha128", dict(dim=256, hidden_dim=320, n_layers=1, n_heads=2, n_kv_heads=2, vocab_size=300, max_seq=1300),
-     "q4_0", [(636, 646), (1277, 1286)]),
+     "q4_0", [(636, 646), (1019, 1029), (1277, 1286)]),
+    # 4 query heads on one kv head of 64 dims (c4's grouping): both one-launch instances and the
+    # two-launch path past 1024 positions
+    ("gqa64", dict(dim=256, hidden_dim=320, n_layers=1, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=1100),
+     "q8_0", [(636, 646), (1019, 1029)]),
     # grouped heads (2 and 8 query heads per kv head), head_dim 32 and 16: the per-query-head P.V
     # kernel reading its kv head's V, whole-context and streamed past 640 positions
     ("gqa32", dict(dim=128, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=1300),
