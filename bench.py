@@ -237,12 +237,10 @@ def measure(q, w, P, K, W, detail=False):
             out["batched_decode"] = batched
             stages = {}
             for st in ("qkv", "wo", "w13", "w2", "output", "attn", "attn_scores", "attn_pv"):
-                if st == "attn" and P + K - 1 >= 640:
-                    continue  # the one-launch attention takes positions below 640
                 try:
                     ms, nbytes = m.time_stage(st, 3 * w.n_layers, pos=P + K - 1)
                 except q.QmhError:
-                    continue  # a head shape the one-launch attention does not take
+                    continue  # a head shape or position the one-launch attention does not take
                 stages[st] = {"us_per_launch": round(ms * 1e3, 3),
                               "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1) if nbytes else None,
                               "weight_MB": round(nbytes / 1e6, 3)}
