@@ -550,19 +550,22 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_pv_mha(const float *__restrict_
 
 // pv_short for the one-launch kernel: the same statistics, products and sums, with the products of
 // every position staged at once (Vs holds the whole context; this thread's exponentials read from
-// LDS together, then its 4*L4 products stored), one barrier, and the chain lanes (the first 16
+// LDS together, then its 4*L4 products stored), one barrier, and the chain lanes (the first CW
 // threads) adding the n products of their column in order without further barriers
-// (qmh_chain_lds: float4 reads two sets of 32 ahead of the adds).
-template <int TC>
+// (qmh_chain_lds: float4 reads two sets of 32 ahead of the adds). CW output columns (16 or 8): thread
+// tid holds V columns 4*(tid % (CW/4)) .. +3 of positions k*PR + tid / (CW/4), PR = 4*256/CW.
+template <int TC, int CW>
 __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1) / QMH_WG],
-                                              float4 (&vv)[TC * QMH_PV_CW / 4 / QMH_WG], uint64_t etv,
+                                              float4 (&vv)[TC * CW / 4 / QMH_WG], uint64_t etv,
                                               const float *x0p, int n, int h, int i0, int hd,
                                               float *__restrict__ out, float *pv_smem) {
-    constexpr int VS = TC + 4;                       // staged row stride == 4 mod 64 floats
-    constexpr int L4 = TC * QMH_PV_CW / 4 / QMH_WG;  // float4 V loads per thread
-    constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;   // scores per thread
+    constexpr int VS = TC + 4;                      // staged row stride == 4 mod 64 floats
+    constexpr int L4 = TC * CW / 4 / QMH_WG;        // float4 V loads per thread
+    constexpr int SK = (TC + QMH_WG - 1) / QMH_WG;  // scores per thread
     constexpr int NW = QMH_WG / 64;
-    static_assert(TC % 32 == 0 && L4 * (QMH_WG / 4) == TC, "every position staged, whole 32-position steps");
+    constexpr int TPP = CW / 4, PR = QMH_WG / TPP;  // threads per position, positions per round
+    static_assert((CW == 16 || CW == 8) && TC % 32 == 0 && L4 * PR == TC,
+                  "every position staged, whole 32-position steps");
     float *P = pv_smem;       // [TC] exponentials e_t
     float *Vs = pv_smem + TC; // [CW][VS] products, transposed
     __shared__ float wmax[NW];
@@ -615,23 +618,23 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
     float pj[L4];
 #pragma unroll
     for (int k = 0; k < L4; k++) {
-        const int t = k * (QMH_WG / 4) + (tid >> 2);
+        const int t = k * PR + tid / TPP;
         pj[k] = t < n ? P[t] : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < L4; k++) {
-        const int t = k * (QMH_WG / 4) + (tid >> 2);
+        const int t = k * PR + tid / TPP;
         const bool on = t < n;
         const float p = pj[k] * inv;
         const float4 v = vv[k];
-        float *dst = Vs + (size_t)(4 * (tid & 3)) * VS + t;
+        float *dst = Vs + (size_t)(4 * (tid % TPP)) * VS + t;
         dst[0] = on ? p * v.x : 0.0f;
         dst[VS] = on ? p * v.y : 0.0f;
         dst[2 * VS] = on ? p * v.z : 0.0f;
         dst[3 * VS] = on ? p * v.w : 0.0f;
     }
     __syncthreads();
-    if (tid < QMH_PV_CW) {  // out = out + p_t*v_t in t order
+    if (tid < CW) {  // out = out + p_t*v_t in t order
         const float acc = qmh_chain_lds(Vs + (size_t)tid * VS, n, 0.0f);
         if (i0 + tid < hd) out[(size_t)h * hd + i0 + tid] = acc;
     }
@@ -669,21 +672,22 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 #define QMH_AF_TC 640
 #define QMH_AF_TC2 1024
 #define QMH_AF_SPIN (1u << 16)
-// workgroups of k_attn_fused's grid: 8 XCDs x ceil(n_heads / 8) heads x head_dim/16
-__host__ __device__ __forceinline__ int af_grid(int n_heads, int hd) { return 8 * ((n_heads + 7) / 8) * (hd / QMH_PV_CW); }
+// workgroups of k_attn_fused's grid: 8 XCDs x ceil(n_heads / 8) heads x head_dim/cw
+__host__ __device__ __forceinline__ int af_grid(int n_heads, int hd, int cw) { return 8 * ((n_heads + 7) / 8) * (hd / cw); }
 
-template <int HD, int TC>
+template <int HD, int TC, int CW>
 __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ Kt,
                                                        const float *__restrict__ V, float *__restrict__ out,
                                                        uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync,
                                                        int n_heads, int n_kv, int max_seq, float scale, int layer,
                                                        int n_layers, uint32_t spin, uint32_t skew) {
-    constexpr int CW = QMH_PV_CW, NCG = HD / CW;
+    constexpr int NCG = HD / CW, TPP = CW / 4, PR = QMH_WG / TPP;  // column groups; V: threads per position
     constexpr int SPM = ((TC + NCG - 1) / NCG + 3) / 4 * 4;          // most positions of one slice
     constexpr int KS = HD + 4;                                       // LDS row stride of the K slice
     constexpr int KL4 = (SPM / 4 * HD + QMH_WG - 1) / QMH_WG;        // float4 K loads per thread
     constexpr int L4 = TC * CW / 4 / QMH_WG, SK = (TC + QMH_WG - 1) / QMH_WG;
     static_assert(HD % CW == 0 && SPM <= QMH_WG, "whole column groups; one chain lane per position");
+    static_assert(CW == 16 || CW == 8, "16 or 8 output columns per workgroup");
     extern __shared__ __align__(16) float af_smem[];
     __shared__ __align__(16) float qs[HD];
     __shared__ float x0s;
@@ -715,16 +719,16 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
         kv[k] = qmh_ld_nt4(kb + (size_t)d * max_seq + tc);
     }
     const uint64_t etv = tid < 32 ? qmh_exp2_tab[tid] : 0;
-    // V (position k*64 + tid/4, columns c .. c+3), loaded non-temporally right behind K: K's
+    // V (position k*PR + tid/TPP, columns c .. c+3), loaded non-temporally right behind K: K's
     // arrival waits only for K (the vector-memory counter retires loads in order), and the barrier
     // after the K slice's staging waits for LDS alone, so V streams under the score chains and the
     // poll (measured on MI355X: the poll's results come back behind V either way)
-    const int c = i0 + 4 * (tid & 3), cc = c <= HD - 4 ? c : HD - 4;
+    const int c = i0 + 4 * (tid % TPP), cc = c <= HD - 4 ? c : HD - 4;
     float4 vv[L4];
     auto vload = [&] {
 #pragma unroll
         for (int k = 0; k < L4; k++) {
-            const int t = k * (QMH_WG / 4) + (tid >> 2), tcl = t < n ? t : n - 1;
+            const int t = k * PR + tid / TPP, tcl = t < n ? t : n - 1;
             vv[k] = qmh_ld_nt4(V + (size_t)tcl * kvd + (size_t)kvh * HD + cc);
         }
     };
@@ -801,35 +805,59 @@ __global__ __launch_bounds__(QMH_WG) void k_attn_fused(const float *__restrict__
     for (int k = 0; k < SK; k++) sv[k] = __uint_as_float((uint32_t)w[k]);
     if (tid == 0) x0s = sv[0];
     __syncthreads();  // the K slice is dead: its LDS is the V sum's from here
-    pv_short_flow<TC>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
+    pv_short_flow<TC, CW>(sv, vv, etv, &x0s, n, h, i0, HD, out, af_smem);
 }
 
-// dynamic LDS bytes of k_attn_fused<HD, TC>: the larger of the K slice and the V sum's buffers
-static size_t af_lds_bytes(int hd, int tc) {
-    const int ncg = hd / QMH_PV_CW, spm = ((tc + ncg - 1) / ncg + 3) / 4 * 4;
-    const size_t kslice = (size_t)spm * (hd + 4), pv = (size_t)tc + QMH_PV_CW * (size_t)(tc + 4);
+// dynamic LDS bytes of k_attn_fused<HD, TC, CW>: the larger of the K slice and the V sum's buffers
+static size_t af_lds_bytes(int hd, int tc, int cw) {
+    const int ncg = hd / cw, spm = ((tc + ncg - 1) / ncg + 3) / 4 * 4;
+    const size_t kslice = (size_t)spm * (hd + 4), pv = (size_t)tc + (size_t)cw * (size_t)(tc + 4);
     return sizeof(float) * (kslice > pv ? kslice : pv);
 }
 
 extern "C" int qmh_attn_fused_max_n(int instance) { return instance == 0 ? QMH_AF_TC : instance == 1 ? QMH_AF_TC2 : 0; }
 
-// the kernel of an instance for a head size, or NULL
-static const void *af_kernel(int head_dim, int instance) {
+// the kernel of an instance for a head size and column width, or NULL. The 1024-position instance
+// needs slices of at most 256 positions (one chain lane each): head_dim / cw >= 4
+typedef void (*af_fn)(const float *, const float *, const float *, float *, uint64_t *, const int32_t *, uint32_t *,
+                      int, int, int, float, int, int, uint32_t, uint32_t);
+template <int CW>
+static af_fn af_kernel_cw(int head_dim, int instance) {
     if (instance == 0)
-        return head_dim == 128 ? (const void *)k_attn_fused<128, QMH_AF_TC>
-               : head_dim == 64 ? (const void *)k_attn_fused<64, QMH_AF_TC>
-               : head_dim == 48 ? (const void *)k_attn_fused<48, QMH_AF_TC> : NULL;
-    if (instance == 1)
-        return head_dim == 128 ? (const void *)k_attn_fused<128, QMH_AF_TC2>
-               : head_dim == 64 ? (const void *)k_attn_fused<64, QMH_AF_TC2> : NULL;
+        return head_dim == 128 ? k_attn_fused<128, QMH_AF_TC, CW>
+               : head_dim == 64 ? k_attn_fused<64, QMH_AF_TC, CW>
+               : head_dim == 48 ? k_attn_fused<48, QMH_AF_TC, CW> : NULL;
+    if (instance == 1) {
+        if (head_dim == 128) return k_attn_fused<128, QMH_AF_TC2, CW>;
+        if (head_dim == 64) return k_attn_fused<64, QMH_AF_TC2, CW>;
+        if constexpr (CW == 8)
+            if (head_dim == 48) return k_attn_fused<48, QMH_AF_TC2, 8>;
+    }
     return NULL;
 }
+static af_fn af_kernel(int head_dim, int instance, int cw) {
+    return cw == 16 ? af_kernel_cw<16>(head_dim, instance) : cw == 8 ? af_kernel_cw<8>(head_dim, instance) : NULL;
+}
 
-// the number of instances k_attn_fused takes the shape with (0, 1: contexts up to 640, 2: also up to
-// 1024): head_dim 48, 64 or 128 (the second instance: 64 or 128), max_seq a whole number of float4s,
-// and no more workgroups than the device holds at once (every head's workgroups run together)
-extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
-    if (max_seq % 4 || max_seq < 4 || n_kv_heads < 1 || n_heads % n_kv_heads || !af_kernel(head_dim, 0)) return 0;
+// the output columns per workgroup k_attn_fused runs a shape with: 8 when the grid of 8-column
+// workgroups still fits the device one workgroup per CU (twice the workgroups, each loading half
+// the K slice and half the V columns: a workgroup's loads are bound by its own CU, not by HBM,
+// while half of the CUs would idle), else 16; 0 for a head size it does not take
+extern "C" int qmh_attn_fused_cw(int n_heads, int head_dim) {
+    if (!af_kernel(head_dim, 0, 16) || n_heads < 1) return 0;
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return (long long)af_grid(n_heads, head_dim, 8) <= (long long)ncu ? 8 : 16;
+}
+
+// the number of instances k_attn_fused takes the shape with at column width cw (0, 1: contexts up to
+// 640, 2: also up to 1024): head_dim 48, 64 or 128 (the second instance: 64 or 128, and 48 at 8
+// columns), max_seq a whole number of float4s, and no more workgroups than the device holds at once
+// (every head's workgroups run together)
+extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq, int cw) {
+    if (max_seq % 4 || max_seq < 4 || n_kv_heads < 1 || n_heads % n_kv_heads || !af_kernel(head_dim, 0, cw)) return 0;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -837,38 +865,31 @@ extern "C" int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_di
     int count = 0;
     for (int i = 0; i < 2; i++) {
         int per = 0;
-        const void *k = af_kernel(head_dim, i);
-        if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, QMH_WG, af_lds_bytes(head_dim, qmh_attn_fused_max_n(i))) !=
-                      hipSuccess ||
-            (long long)af_grid(n_heads, head_dim) > (long long)per * ncu)
+        const af_fn k = af_kernel(head_dim, i, cw);
+        if (!k ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k, QMH_WG,
+                                                         af_lds_bytes(head_dim, qmh_attn_fused_max_n(i), cw)) != hipSuccess ||
+            (long long)af_grid(n_heads, head_dim, cw) > (long long)per * ncu)
             break;
         count = i + 1;
     }
     return count;
 }
 
-// the caller has checked qmh_attn_fused_supported for the shape and instance; stall != 0 (tests
-// only): the readers wait for an epoch nobody writes, for 64 polls
+// the caller has checked qmh_attn_fused_supported for the shape, column width and instance; stall !=
+// 0 (tests only): the readers wait for an epoch nobody writes, for 64 polls
 extern "C" int qmh_launch_attn_fused(const float *q, const float *kcache, const float *vcache, float *out,
                                      uint64_t *attp, const int32_t *pos_ptr, uint32_t *sync, int n_heads,
                                      int n_kv_heads, int head_dim, int max_seq, float scale, int layer, int n_layers,
-                                     int instance, int stall, void *stream) {
-    const void *k = af_kernel(head_dim, instance);
+                                     int instance, int cw, int stall, void *stream) {
+    const af_fn k = af_kernel(head_dim, instance, cw);
     if (!k || max_seq % 4 || max_seq < 4 || n_kv_heads < 1 || n_heads % n_kv_heads) return (int)hipErrorNotSupported;
-    const dim3 grid(af_grid(n_heads, head_dim));
-    const size_t lds = af_lds_bytes(head_dim, qmh_attn_fused_max_n(instance));
+    const dim3 grid(af_grid(n_heads, head_dim, cw));
+    const size_t lds = af_lds_bytes(head_dim, qmh_attn_fused_max_n(instance), cw);
     hipStream_t s = (hipStream_t)stream;
     const uint32_t spin = stall ? 64u : QMH_AF_SPIN, skew = stall ? 1u : 0u;
-#define QMH_AF(HD, TC)                                                                                            \
-    hipLaunchKernelGGL((k_attn_fused<HD, TC>), grid, dim3(QMH_WG), lds, s, q, kcache, vcache, out, attp, pos_ptr, \
-                       sync, n_heads, n_kv_heads, max_seq, scale, layer, n_layers, spin, skew)
-    if (instance == 1) {
-        if (head_dim == 128) QMH_AF(128, QMH_AF_TC2);
-        else QMH_AF(64, QMH_AF_TC2);
-    } else if (head_dim == 128) QMH_AF(128, QMH_AF_TC);
-    else if (head_dim == 64) QMH_AF(64, QMH_AF_TC);
-    else QMH_AF(48, QMH_AF_TC);
-#undef QMH_AF
+    hipLaunchKernelGGL(k, grid, dim3(QMH_WG), lds, s, q, kcache, vcache, out, attp, pos_ptr, sync, n_heads, n_kv_heads,
+                       max_seq, scale, layer, n_layers, spin, skew);
     return (int)hipGetLastError();
 }
 

@@ -87,13 +87,16 @@ int qmh_launch_attn_pv(const float *att, const float *vtcache, float *out, const
  * qmh_attn_fused_max_n(instance) positions (instance 0: 640, 1: 1024): scores exchanged between a
  * head's workgroups as epoch-tagged words in attp [n_heads][max_seq] (zeroed at allocation); sync[0]
  * counts decode steps (qmh_launch_embed), sync[1] != 0 reports a bounded wait that ran out (or a
- * launch past the instance's context limit). qmh_attn_fused_supported: how many instances take the
- * shape (0, 1 or 2) */
+ * launch past the instance's context limit). Each workgroup owns cw output columns of a head (16
+ * or 8; qmh_attn_fused_cw: the width for the shape on this device). qmh_attn_fused_supported: how
+ * many instances take the shape at that width (0, 1 or 2) */
 int qmh_attn_fused_max_n(int instance);
-int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq);
+int qmh_attn_fused_cw(int n_heads, int head_dim);
+int qmh_attn_fused_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq, int cw);
 int qmh_launch_attn_fused(const float *q, const float *kcache, const float *vcache, float *out, uint64_t *attp,
                           const int32_t *pos_ptr, uint32_t *sync, int n_heads, int n_kv_heads, int head_dim,
-                          int max_seq, float scale, int layer, int n_layers, int instance, int stall, void *stream);
+                          int max_seq, float scale, int layer, int n_layers, int instance, int cw, int stall,
+                          void *stream);
 /* the decode attention kernels over B sequences of a batched step (MHA, head_dim 128/64/48; else
  * hipErrorNotSupported): query Q[b][n_heads*hd], caches at Kt/V + b*kv_stride, position pos[b],
  * scores att[b][n_heads][max_seq], out[b][n_heads*hd] */

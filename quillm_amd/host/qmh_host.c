@@ -396,6 +396,7 @@ struct qmh_model {
     hipGraphExec_t exec_fwd_af[2], exec_greedy_af[2];
     int af_n;          /* k_attn_fused's instances that take the model's shape (0: none) */
     int af_inst;       /* the instance ST_ATTN launches */
+    int af_cw;         /* its output columns per workgroup (16 or 8) */
     int af_stall;      /* QMH_AF_FORCE_STALL (tests): the one-launch attention's waits run out */
     uint64_t *d_attp;  /* [n_heads][max_seq] epoch-tagged scores of k_attn_fused */
     uint32_t *d_sync;  /* [0] decode steps (k_embed), [1] k_attn_fused's wait status */
@@ -446,8 +447,8 @@ static int enqueue_stage(qmh_model *m, int which, int l, hipStream_t s) {
     case ST_ATTN: /* src/model.c:137-156 in one launch */
         if (m->af_inst >= m->af_n) return (int)hipErrorNotSupported;
         return qmh_launch_attn_fused(m->d_q, kl, vl, m->d_xb, m->d_attp, pos_ptr, m->d_sync, c->n_heads, c->n_kv_heads,
-                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), l, c->n_layers, m->af_inst, m->af_stall,
-                                     s);
+                                     m->hd, S_, 1.0f / sqrtf((float)m->hd), l, c->n_layers, m->af_inst, m->af_cw,
+                                     m->af_stall, s);
     case ST_WO: /* x += Wo xb (src/model.c:178-179) */
         mv_args_for(&L->wo, &a);
         a.x = m->d_xb;
@@ -852,7 +853,13 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
     HIPCHK(hipMemsetAsync(m->d_v, 0, kv_bytes, g_stream));
     HIPCHK(hipMemsetAsync(m->d_tokpos, 0, sizeof(int32_t) * 4, g_stream));
     /* the one-launch attention: its score words start at epoch 0, which no launch uses */
-    m->af_n = getenv("QMH_NO_FUSED_ATTN") ? 0 : qmh_attn_fused_supported(c->n_heads, c->n_kv_heads, m->hd, (int)S_);
+    {
+        /* QMH_AF_CW=16 or 8 (tests): the column width instead of the one chosen for the shape */
+        const char *cw = getenv("QMH_AF_CW");
+        m->af_cw = cw && (atoi(cw) == 16 || atoi(cw) == 8) ? atoi(cw) : qmh_attn_fused_cw(c->n_heads, m->hd);
+    }
+    m->af_n = getenv("QMH_NO_FUSED_ATTN") ? 0
+                                          : qmh_attn_fused_supported(c->n_heads, c->n_kv_heads, m->hd, (int)S_, m->af_cw);
     if (m->af_n > 1 && getenv("QMH_FUSED_ATTN_640")) m->af_n = 1;
     m->af_stall = getenv("QMH_AF_FORCE_STALL") != NULL;
     HIPCHK(hipMalloc((void **)&m->d_sync, sizeof(uint32_t) * 2));

@@ -17,8 +17,9 @@ passes. The formulas restate the kernels' own index arithmetic, line by line:
   * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:393-530: one workgroup per query head, float4 V
                           loads of its kv head clamped to position n-1 and column head_dim-4
   * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:532-555: kernel choice and dynamic LDS
-  * k_attn_fused<HD,TC>   quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= TC, TC 640
-                          for head_dim 48/64/128 and 1024 for head_dim 64/128): the K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
+  * k_attn_fused<HD,TC,CW> quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= TC, TC 640
+                          for head_dim 48/64/128 and 1024 for head_dim 64/128 (48 too at CW 8), CW =
+                          16 or 8 output columns per workgroup): the K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
                           score words, and that the slices of a head's workgroups cover its n
                           positions exactly once (a position nobody writes would leave its readers
                           waiting until their bounded wait runs out)
@@ -216,31 +217,37 @@ AF_TC = 640
 AF_TC2 = 1024  # the second instance (head_dim 64 and 128)
 
 
-def af_instances(hd):
-    """The instances (their TC) qmh_attn_fused_supported can return for a head size."""
-    return [AF_TC, AF_TC2] if hd in (64, 128) else [AF_TC] if hd == 48 else []
+def af_instances(hd, cw=CW):
+    """The instances (their TC) qmh_attn_fused_supported can return for a head size and column width
+    (af_kernel_cw)."""
+    if hd not in (48, 64, 128):
+        return []
+    return [AF_TC, AF_TC2] if hd in (64, 128) or cw == 8 else [AF_TC]
 
 
-def af_lds_floats(hd, TC):
-    ncg = hd // CW
+def af_lds_floats(hd, TC, cw=CW):
+    ncg = hd // cw
     spm = ((TC + ncg - 1) // ncg + 3) // 4 * 4
-    return max(spm * (hd + 4), TC + CW * (TC + 4))
+    return max(spm * (hd + 4), TC + cw * (TC + 4))
 
 
-def fused(nh, nkv, hd, S, n, ext, TC=AF_TC):
-    """k_attn_fused<HD,TC> over its (head, column group) workgroups x 256 threads (the grid's
+def fused(nh, nkv, hd, S, n, ext, TC=AF_TC, cw=CW):
+    """k_attn_fused<HD,TC,CW> over its (head, column group) workgroups x 256 threads (the grid's
     placement: af_grid_map), n <= TC positions: every thread loads its
-    part of the K slice and its V float4s (as k_attn_pv_mha), the threads below the slice's position
-    count run the score chains, every thread reads the head's scores, stages its products for all TC
-    positions, and the first 16 threads run the V sum's chains (pv_short_flow)."""
-    assert TC in af_instances(hd) and S % 4 == 0 and S >= 4 and n <= min(TC, S)
+    part of the K slice and its V float4s (as k_attn_pv_mha, TPP = CW/4 threads per position), the
+    threads below the slice's position count run the score chains, every thread reads the head's
+    scores, stages its products for all TC positions, and the first CW threads run the V sum's chains
+    (pv_short_flow)."""
+    assert cw in (16, 8) and TC in af_instances(hd, cw) and S % 4 == 0 and S >= 4 and n <= min(TC, S)
     AF_TC = TC
-    ncg, kvd = hd // CW, hd * nkv
+    ncg, kvd = hd // cw, hd * nkv
+    TPP = cw // 4
+    PR = WG // TPP
     spm = ((AF_TC + ncg - 1) // ncg + 3) // 4 * 4
     KS, KL4 = hd + 4, (spm // 4 * hd + WG - 1) // WG
-    L4, SK, VS = AF_TC * CW // 4 // WG, (AF_TC + WG - 1) // WG, AF_TC + 4
-    assert spm <= WG and L4 * (WG // 4) == AF_TC
-    lds = af_lds_floats(hd, TC)
+    L4, SK, VS = AF_TC * cw // 4 // WG, (AF_TC + WG - 1) // WG, AF_TC + 4
+    assert spm <= WG and L4 * PR == AF_TC
+    lds = af_lds_floats(hd, TC, cw)
     assert 4 * lds <= LDS_MAX
     tid = np.arange(WG)
     inb("af q", np.arange(nh)[:, None] * hd + 4 * tid[tid < hd // 4][None, :] + 3, ext.q)
@@ -267,10 +274,10 @@ def fused(nh, nkv, hd, S, n, ext, TC=AF_TC):
         for h in range(nh):
             inb("af score word", h * S + p0 + rows, ext.att)
         covered[p0 + rows] += 1
-        # V: position k*64 + tid/4 clamped to n-1, columns i0 + 4*(tid%4) clamped to hd-4
-        c = cg * CW + 4 * (tid & 3)
+        # V: position k*PR + tid/TPP clamped to n-1, columns i0 + 4*(tid%TPP) clamped to hd-4
+        c = cg * cw + 4 * (tid % TPP)
         cc = np.where(c <= hd - 4, c, hd - 4)
-        tv = np.minimum(np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :], n - 1)
+        tv = np.minimum(np.arange(L4)[:, None] * PR + (tid // TPP)[None, :], n - 1)
         for kvh in range(nkv):
             for r in range(4):
                 inb("af V", tv * kvd + kvh * hd + cc[None, :] + r, ext.V)
@@ -278,15 +285,20 @@ def fused(nh, nkv, hd, S, n, ext, TC=AF_TC):
     t = tid[None, :] + WG * np.arange(SK)[:, None]
     inb("af poll", np.arange(nh)[:, None] * S + t[t < n][None, :], ext.att)
     inb("af P", t[t < n], AF_TC)
-    # staging: every thread, positions k*64 + tid/4 (all < TC), rows 4*(tid%4) + r of Vs
-    ts = np.arange(L4)[:, None] * (WG // 4) + (tid >> 2)[None, :]
+    # staging: every thread, positions k*PR + tid/TPP (all < TC), rows 4*(tid%TPP) + r of Vs
+    ts = np.arange(L4)[:, None] * PR + (tid // TPP)[None, :]
     assert ts.max() < AF_TC
     inb("af P read", ts[ts < n], AF_TC)
     for r in range(4):
-        inb("af stage", AF_TC + (4 * (tid & 3) + r)[None, :] * VS + ts, lds)
-    # chains: 16 lanes, 32-position steps up to the last holding a position below n
+        inb("af stage", AF_TC + (4 * (tid % TPP) + r)[None, :] * VS + ts, lds)
+    # every (column, position) cell below TC staged exactly once
+    cells = np.zeros((cw, AF_TC), dtype=np.int64)
+    for r in range(4):
+        np.add.at(cells, (np.broadcast_to((4 * (tid % TPP) + r)[None, :], ts.shape), ts), 1)
+    assert (cells == 1).all()
+    # chains: CW lanes, 32-position steps up to the last holding a position below n
     nst = (n + 31) >> 5
-    inb("af chain", AF_TC + np.arange(CW)[:, None] * VS + 4 * (8 * (nst - 1) + np.arange(8))[None, :] + 3, lds)
+    inb("af chain", AF_TC + np.arange(cw)[:, None] * VS + 4 * (8 * (nst - 1) + np.arange(8))[None, :] + 3, lds)
     assert 32 * nst <= AF_TC
     mha_out(nh, hd, ext)
 
@@ -324,28 +336,30 @@ def test_decode_attention_indices_in_bounds(shape):
         # positions the host gives it (below 640: the first; 640..1023: the second) and the first
         # at every position below 640
         if S % 4 == 0 and S >= 4:
-            for TC in af_instances(hd):
-                if pos + 1 <= TC:
-                    fused(nh, nkv, hd, S, pos + 1, ext, TC)
+            for cw in (16, 8):
+                for TC in af_instances(hd, cw):
+                    if pos + 1 <= TC:
+                        fused(nh, nkv, hd, S, pos + 1, ext, TC, cw)
 
 
+@pytest.mark.parametrize("cw", [16, 8])
 @pytest.mark.parametrize("TC", [AF_TC, AF_TC2])
-def test_fused_slices_cover_every_position(TC):
+def test_fused_slices_cover_every_position(TC, cw):
     """Every n in 1..TC and every head_dim the instance takes: its workgroups' score slices
     cover positions 0..n-1 once each (fused() asserts it), here with the other checks too."""
     for hd in (48, 64, 128):
-        if TC not in af_instances(hd):
+        if TC not in af_instances(hd, cw):
             continue
         ext = Extents(2, 1, hd, TC)
         for n in range(1, TC + 1):
-            fused(2, 1, hd, TC, n, ext, TC)
+            fused(2, 1, hd, TC, n, ext, TC, cw)
 
 
-def af_grid_map(nh, hd):
-    """k_attn_fused's one-dimensional grid: 8 * ceil(nh/8) * (hd/16) workgroups; workgroup L takes
+def af_grid_map(nh, hd, cw=CW):
+    """k_attn_fused's one-dimensional grid: 8 * ceil(nh/8) * (hd/cw) workgroups; workgroup L takes
     head (L % 8) * ceil(nh/8) + (L / 8) / ncg, column group (L / 8) % ncg, and returns when the head
     is past nh. (h, cg) of each workgroup, -1 for the ones that return."""
-    ncg = hd // CW
+    ncg = hd // cw
     hpx = (nh + 7) // 8
     G = 8 * hpx * ncg
     L = np.arange(G)
@@ -354,17 +368,18 @@ def af_grid_map(nh, hd):
     return L, np.where(h < nh, h, -1), np.where(h < nh, cg, -1)
 
 
+@pytest.mark.parametrize("cw", [16, 8])
 @pytest.mark.parametrize("nh", [1, 2, 4, 6, 8, 12, 25, 32, 64])
 @pytest.mark.parametrize("hd", [48, 64, 128])
-def test_fused_grid_places_each_head_on_one_xcd(nh, hd):
+def test_fused_grid_places_each_head_on_one_xcd(nh, hd, cw):
     """Every (head, column group) has exactly one workgroup, and a head's workgroups have one
     dispatch slot modulo 8 (the XCD the round-robin dispatcher gives them). The heads of one XCD
     are consecutive, so the query heads that share a kv head share as few XCDs as possible:
     ceil(group / heads per XCD) + 1 at most."""
-    L, h, cg = af_grid_map(nh, hd)
+    L, h, cg = af_grid_map(nh, hd, cw)
     live = h >= 0
-    pairs = h[live] * (hd // CW) + cg[live]
-    assert np.array_equal(np.sort(pairs), np.arange(nh * (hd // CW)))
+    pairs = h[live] * (hd // cw) + cg[live]
+    assert np.array_equal(np.sort(pairs), np.arange(nh * (hd // cw)))
     for head in range(nh):
         assert len(set((L[h == head] % 8).tolist())) == 1
     hpx = (nh + 7) // 8

@@ -2,11 +2,13 @@
 
 * The one-launch attention (k_attn_fused: scores, softmax and V sum, the scores exchanged between a
   head's workgroups as epoch-tagged words) against the CPU oracle, at decode positions on both sides
-  of its instances' limits (640 positions; 1024 for head_dim 64 and 128), for the head shapes it
-  takes (head_dim 128, 64 and 48; one and four query heads per kv head).
+  of its instances' limits (640 positions; 1024 for head_dim 64 and 128, and for 48 at 8 columns per
+  workgroup), for the head shapes it takes (head_dim 128, 64 and 48; one and four query heads per kv
+  head), with 8 output columns per workgroup (the width the library picks for grids that fill at most
+  the device) and 16 (QMH_AF_CW=16, the width of larger models).
 * The same steps replayed from hipGraphs, enqueued kernel by kernel (QMH_NO_GRAPH), with the
-  two-launch attention (QMH_NO_FUSED_ATTN) and with the 640-position instance alone
-  (QMH_FUSED_ATTN_640): identical logits and greedy ids.
+  two-launch attention (QMH_NO_FUSED_ATTN), with the 640-position instance alone
+  (QMH_FUSED_ATTN_640) and with 16 columns per workgroup: identical logits and greedy ids.
 * A rerun of the same decode steps gives the same bits (reference: tests/test_model.c:84-94 reruns a
   model, tests/test_threads.c:56-94 compares thread counts bitwise).
 * The bounded wait of the one-launch attention, run to its end from the host (QMH_AF_FORCE_STALL):
@@ -29,9 +31,10 @@ AF_SHAPES = {
     "af64g": dict(dim=256, hidden_dim=384, n_layers=2, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=664),
     "af48": dict(dim=96, hidden_dim=160, n_layers=2, n_heads=2, n_kv_heads=1, vocab_size=300, max_seq=100),
     "af64x": dict(dim=256, hidden_dim=384, n_layers=2, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=1040),
+    "af48x": dict(dim=96, hidden_dim=160, n_layers=2, n_heads=2, n_kv_heads=1, vocab_size=300, max_seq=700),
 }
 # prompt length and decode steps: the steps cross position 640 (and 1024) where the context allows it
-RUN = {"af128": (630, 20), "af64g": (632, 20), "af48": (60, 30), "af64x": (1014, 20)}
+RUN = {"af128": (630, 20), "af64g": (632, 20), "af48": (60, 30), "af64x": (1014, 20), "af48x": (630, 20)}
 
 
 def bits(a):
@@ -91,16 +94,17 @@ def decode(gpu, path, prompt, n_gen, **kv):
     return first, np.stack(lg), np.asarray(ids)
 
 
+@pytest.mark.parametrize("cw", ["8", "16"])
 @pytest.mark.parametrize("shape", list(AF_SHAPES))
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
-def test_fused_attention_matches_oracle(gpu, oracle, af_models, shape, wt):
+def test_fused_attention_matches_oracle(gpu, oracle, af_models, shape, wt, cw):
     path = af_models[(shape, wt)]
     P, G = RUN[shape]
     prompt = gpu.prompt_ids(P, 300, seed=7)
-    say(f"case {shape}/{wt}: oracle {P}+{G}")
+    say(f"case {shape}/{wt}/cw{cw}: oracle {P}+{G}")
     want, want_ids = oracle.run_model(path, prompt, n_gen=G)
-    say(f"case {shape}/{wt}: device decode positions {P}..{P + G - 1}")
-    first, lg, ids = decode(gpu, path, prompt, G)
+    say(f"case {shape}/{wt}/cw{cw}: device decode positions {P}..{P + G - 1}")
+    first, lg, ids = decode(gpu, path, prompt, G, QMH_AF_CW=cw)
     assert first == int(want_ids[0])
     assert np.array_equal(bits(lg), bits(want[P:])), np.abs(lg - want[P:]).max()
     assert list(ids) == list(want_ids[1:])
@@ -122,7 +126,7 @@ def test_fused_attention_from_position_zero(gpu, oracle, af_models):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("shape", ["af128", "af64g", "af64x"])
+@pytest.mark.parametrize("shape", ["af128", "af64g", "af64x", "af48x"])
 def test_decode_variants_agree(gpu, af_models, shape):
     path = af_models[(shape, "q4_0")]
     P, G = RUN[shape]
@@ -131,6 +135,7 @@ def test_decode_variants_agree(gpu, af_models, shape):
     for name, kv in [("graph+fused", {}), ("no graph", {"QMH_NO_GRAPH": "1"}),
                      ("two-launch attention", {"QMH_NO_FUSED_ATTN": "1"}),
                      ("640-position instance alone", {"QMH_FUSED_ATTN_640": "1"}),
+                     ("16 columns per workgroup", {"QMH_AF_CW": "16"}),
                      ("no graph, two-launch", {"QMH_NO_GRAPH": "1", "QMH_NO_FUSED_ATTN": "1"})]:
         say(f"case {shape}: {name}")
         runs[name] = decode(gpu, path, prompt, G, **kv)
