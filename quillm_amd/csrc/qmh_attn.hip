@@ -643,11 +643,11 @@ __device__ __forceinline__ void pv_short_flow(const float (&sv)[(TC + QMH_WG - 1
 // ============================================================================ one launch per step
 
 // The decode step's whole attention in one launch, for contexts of up to TC positions (two
-// instances: TC = 640 for head_dim 48, 64 and 128; TC = 1024 for head_dim 64 and 128, whose slices
-// of at most 256 positions keep one chain lane per position):
-// workgroup (cg, h) owns query head h's output columns 16*cg .. +15 (as k_attn_pv_mha) and
-// computes the scores of a slice of the head's positions,
-// [cg*sp, cg*sp + sp) with sp = ceil(n / (head_dim/16)) rounded up to 4. Its K slice arrives as
+// instances: TC = 640 for head_dim 48, 64 and 128; TC = 1024 for head_dim 64 and 128, and 48 at
+// CW = 8, whose slices of at most 256 positions keep one chain lane per position):
+// workgroup (cg, h) owns query head h's output columns CW*cg .. +CW-1 (CW = 16 as k_attn_pv_mha,
+// or 8 where that grid fits the device) and computes the scores of a slice of the head's
+// positions, [cg*sp, cg*sp + sp) with sp = ceil(n / (head_dim/CW)) rounded up to 4. Its K slice arrives as
 // float4s of 4 positions of one dimension (all in flight together), is staged in LDS as rows of
 // head_dim + 4 floats (one position per row), and one lane per position runs the score's serial
 // chain over head_dim. The scores go to attp[h][t] as 64-bit words (score bits | epoch << 32)
