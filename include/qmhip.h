@@ -212,7 +212,8 @@ int qmh_model_sample(qmh_model *m, qmh_sampler *s, int32_t token, int32_t pos, i
  * (+residual), 2 = fused RMSNorm+W1|W3 matvec (+SwiGLU), 3 = W2 matvec (+residual), 4 = final
  * RMSNorm+output matvec, 5 = attention scores, 6 = softmax + attention-weighted V sum, 7 = the
  * whole attention in one launch (scores, softmax and V sum; what decode steps use for positions below
- * 640 when the model's head shape allows it; an error for other models). */
+ * 640, and below 1024 for head_dim 64 and 128, when the model's head shape allows it; an error for
+ * other models and positions). */
 
 /* Average device time of `iters` back-to-back launches of one stage at position pos (token 0),
  * from HIP events on the library stream; launch i uses layer i % n_layers, so weight reads come
