@@ -95,6 +95,8 @@ extern "C" int qmh_launch_attn_scores(const float *q, const float *kcache, float
 // positions is then one chunk, every V value of the workgroup requested at once.
 // MHA (one query head per kv head): the staged values are the products p_t*v_t, each rounded
 // as the reference rounds it, so the chain lanes only add.
+// A workgroup takes up to 16 query heads of its kv head (16 lanes per head): a group of g heads
+// runs as ceil(g/16) sub-groups, blockIdx.x = kv head * ceil(g/16) + sub-group.
 template <int TC, bool MHA>
 __device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, const float *__restrict__ V,
                                                float *__restrict__ out, const int n, int n_heads, int n_kv, int hd,
@@ -104,21 +106,23 @@ __device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, co
     constexpr int SVK = 4;  // first head's scores kept in registers: positions < SVK*256
     static_assert(!MHA || TC <= SVK * QMH_WG, "MHA probabilities of the first chunk come from registers");
     extern __shared__ __align__(16) float pv_smem[];
-    float *P = pv_smem;                              // [group][TC] probabilities
-    float *Vs = pv_smem + (n_heads / n_kv) * TC;     // [CW][TC] the chunk (V or, MHA, p*V), transposed
+    const int group = n_heads / n_kv, nsub = (group + 15) >> 4, gsm = group < 16 ? group : 16;
+    float *P = pv_smem;                              // [gs][TC] probabilities
+    float *Vs = pv_smem + gsm * TC;                  // [CW][TC] the chunk (V or, MHA, p*V), transposed
     __shared__ double red[16];
     __shared__ float redf[16];
     __shared__ float mx_s[16], inv_s[16];
-    const int kvh = blockIdx.x, i0 = blockIdx.y * QMH_PV_CW, group = n_heads / n_kv, kvd = hd * n_kv;
+    const int kvh = blockIdx.x / nsub, sub = blockIdx.x % nsub, i0 = blockIdx.y * QMH_PV_CW, kvd = hd * n_kv;
+    const int hb = kvh * group + 16 * sub, gs = group - 16 * sub < 16 ? group - 16 * sub : 16;  // heads hb .. +gs-1
     const int lane_h = threadIdx.x / QMH_PV_CW, col = threadIdx.x % QMH_PV_CW;
-    const bool chain = lane_h < group;
+    const bool chain = lane_h < gs;
     const int colc = i0 + (int)(threadIdx.x % QMH_PV_CW) < hd ? i0 + (int)(threadIdx.x % QMH_PV_CW) : hd - 1;
     constexpr int LPT = QMH_PV_TC * QMH_PV_CW / QMH_WG;  // V loads per thread per chunk
     float acc = 0.0f;
     // the first head's scores (positions tid + 256k), issued first: the statistics wait for them only
     float sv[SVK];
     {
-        const float *s0 = att + (size_t)(kvh * group) * max_seq;
+        const float *s0 = att + (size_t)hb * max_seq;
 #pragma unroll
         for (int k = 0; k < SVK; k++) {
             const int t = (int)threadIdx.x + k * QMH_WG;
@@ -136,9 +140,9 @@ __device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, co
         vv[k] = V[(size_t)tcl * kvd + kvh * hd + colc];                 \
     }
     QMH_PV_LOAD(0);
-    // softmax statistics per head of the group (src/ops.c:100-112)
-    for (int hl = 0; hl < group; hl++) {
-        const float *s = att + (size_t)(kvh * group + hl) * max_seq;
+    // softmax statistics per head of the sub-group (src/ops.c:100-112)
+    for (int hl = 0; hl < gs; hl++) {
+        const float *s = att + (size_t)(hb + hl) * max_seq;
         float xv[SVK];
 #pragma unroll
         for (int k = 0; k < SVK; k++) {
@@ -189,10 +193,10 @@ __device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, co
                 if (t < QMH_PV_TC) P[t] = t < nt ? qmh_expf(sv[k] - m0) * inv0 : 0.0f;
             }
         } else {
-            for (int e = threadIdx.x; e < group * QMH_PV_TC; e += QMH_WG) {
+            for (int e = threadIdx.x; e < gs * QMH_PV_TC; e += QMH_WG) {
                 const int hl = e / QMH_PV_TC, t = e % QMH_PV_TC;
                 float p = 0.0f;
-                if (t < nt) p = qmh_expf(att[(size_t)(kvh * group + hl) * max_seq + t0 + t] - mx_s[hl]) * inv_s[hl];
+                if (t < nt) p = qmh_expf(att[(size_t)(hb + hl) * max_seq + t0 + t] - mx_s[hl]) * inv_s[hl];
                 P[hl * QMH_PV_TC + t] = p;
             }
         }
@@ -248,7 +252,7 @@ __device__ __forceinline__ void attn_pv_chunks(const float *__restrict__ att, co
         }
         __syncthreads();
     }
-    if (chain && i0 + col < hd) out[(size_t)(kvh * group + lane_h) * hd + i0 + col] = acc;
+    if (chain && i0 + col < hd) out[(size_t)(hb + lane_h) * hd + i0 + col] = acc;
 #undef QMH_PV_LOAD
 }
 
@@ -895,12 +899,13 @@ extern "C" int qmh_launch_attn_fused(const float *q, const float *kcache, const 
 
 extern "C" int qmh_launch_attn_pv(const float *att, const float *vcache, float *out, const int32_t *pos_ptr,
                                   int n_heads, int n_kv_heads, int head_dim, int max_seq, void *stream) {
-    const int group = n_heads / n_kv_heads;
-    if (group > 16 || group * QMH_PV_CW > QMH_WG) return (int)hipErrorInvalidValue;
-    dim3 grid(n_kv_heads, (head_dim + QMH_PV_CW - 1) / QMH_PV_CW);
+    if (n_kv_heads < 1 || n_heads % n_kv_heads) return (int)hipErrorInvalidValue;
+    // k_attn_pv: sub-groups of up to 16 query heads per workgroup (16 lanes each)
+    const int group = n_heads / n_kv_heads, nsub = (group + 15) / 16, gsm = group < 16 ? group : 16;
+    dim3 grid(n_kv_heads * nsub, (head_dim + QMH_PV_CW - 1) / QMH_PV_CW);
     hipStream_t s = (hipStream_t)stream;
 #define QMH_PV_GO(TC, MHA)                                                                                \
-    hipLaunchKernelGGL((k_attn_pv<TC, MHA>), grid, dim3(QMH_WG), sizeof(float) * ((size_t)group * TC + QMH_PV_CW * (TC + 4)), \
+    hipLaunchKernelGGL((k_attn_pv<TC, MHA>), grid, dim3(QMH_WG), sizeof(float) * ((size_t)gsm * TC + QMH_PV_CW * (TC + 4)), \
                        s, att, vcache, out, pos_ptr, n_heads, n_kv_heads, head_dim, max_seq)
     if (head_dim % 4 == 0 && (group == 1 || max_seq <= QMH_PV_LONG)) {
         // one workgroup per query head; the larger of the two paths' LDS: the whole-context one

@@ -786,8 +786,11 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
         D > qmh_matvec_max_cols(1) || H > qmh_matvec_max_cols(0))
         return fail("model dims exceed the kernels' limits (dim <= %d, hidden_dim <= %d)", qmh_matvec_max_cols(1),
                     qmh_matvec_max_cols(0));
-    if (((int64_t)64 * (m->hd + 1) + (int64_t)m->group * m->hd) * 4 > 65536 || m->group > 15)
-        return fail("head_dim/group too large for the attention kernels");
+    /* any group (the reference's only rule is n_heads % n_kv_heads == 0): the kv-head P.V kernel takes
+     * it in sub-groups of up to 16 query heads */
+    const int64_t gsub = m->group < 16 ? m->group : 16;
+    if (((int64_t)64 * (m->hd + 1) + gsub * m->hd) * 4 > 65536)
+        return fail("head_dim too large for the attention kernels");
 
     HIPCHK(hipMalloc(&m->d_embd, (size_t)V * qlm_row_bytes(tok_embd->dtype, D)));
     HIPCHK(hipMemcpy(m->d_embd, tok_embd->data, (size_t)V * qlm_row_bytes(tok_embd->dtype, D), hipMemcpyHostToDevice));

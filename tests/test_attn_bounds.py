@@ -36,6 +36,8 @@ SHAPES = [
     (4, 2, 16, 64), (6, 3, 12, 64), (3, 3, 32, 48), (12, 1, 8, 300), (4, 2, 48, 136),
     (2, 2, 128, 1300), (6, 6, 10, 700), (4, 2, 32, 700), (32, 32, 128, 640),
     (4, 2, 16, 9000), (2, 2, 16, 9000), (8, 1, 12, 8192), (4, 4, 64, 8193),
+    # groups past 16 query heads per kv head: the kv-head P.V kernel in sub-groups of 16
+    (20, 1, 10, 300), (32, 1, 64, 1040), (40, 2, 6, 700), (32, 1, 16, 9000),
 ]
 POSITIONS = [0, 1, 2, 3, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 575, 639, 640, 641, 700,
              767, 768, 1023, 1024, 1279, 1280, 1281, 2047, 4095, 8191, 8192, 8193, 8900]
@@ -93,14 +95,25 @@ def scores(nh, nkv, hd, S, pos, ext):
 
 
 def pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats):
-    """attn_pv_chunks<TC, MHA> over grid (nkv, ceil(hd/16)) x 256 threads."""
+    """attn_pv_chunks<TC, MHA> over grid (nkv * ceil(group/16), ceil(hd/16)) x 256 threads: workgroup x
+    takes kv head x / nsub and query heads hb .. hb + gs - 1 of it, hb = kvh*group + 16*(x % nsub)."""
     group, kvd = nh // nkv, hd * nkv
+    for sub in range((group + 15) // 16):
+        pv_chunks_sub(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats, sub)
+
+
+def pv_chunks_sub(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats, sub):
+    group, kvd = nh // nkv, hd * nkv
+    gsm = min(group, 16)
+    gs = min(16, group - 16 * sub)
+    assert gs >= 1 and gs * CW <= WG
     tid = np.arange(WG)
     kvh = np.arange(nkv)
+    hb = kvh * group + 16 * sub  # first query head of each workgroup
     i0 = np.arange(0, hd, CW)
     # first head's scores, 4 per thread, clamped to 0
     t = tid[None, :] + WG * np.arange(4)[:, None]
-    inb("pv sv", (kvh[:, None] * group) * S + np.where(t < n, t, 0).ravel()[None, :], ext.att)
+    inb("pv sv", hb[:, None] * S + np.where(t < n, t, 0).ravel()[None, :], ext.att)
     LPT = TC * CW // WG
     e = (np.arange(LPT)[:, None] * WG + tid[None, :]).ravel()
     te, cce = e // CW, e % CW
@@ -110,23 +123,25 @@ def pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats):
         inb("pv V", tcl[None, None, :] * kvd + kvh[:, None, None] * hd + colc_e[None, :, :], ext.V)
         nt = min(TC, n - T0)
         if not (MHA and T0 == 0):
-            hl, tt = e[e < group * TC] // TC, e[e < group * TC] % TC
-            inb("pv P", hl * TC + tt, group * TC)
+            hl, tt = e[e < gs * TC] // TC, e[e < gs * TC] % TC
+            inb("pv P", hl * TC + tt, gsm * TC)
             tt_on = tt < nt
-            inb("pv att", (kvh[:, None] * group + hl[None, tt_on]) * S + T0 + tt[None, tt_on], ext.att)
+            inb("pv att", (hb[:, None] + hl[None, tt_on]) * S + T0 + tt[None, tt_on], ext.att)
+            # the sub-group's heads stay inside the kv head's group
+            assert (hl < gs).all() and 16 * sub + gs <= group
         else:
             tp = tid[None, :] + WG * np.arange(4)[:, None]
-            inb("pv P first", tp[tp < TC], group * TC)
-        inb("pv Vs", group * TC + cce * (TC + 4) + te, lds_floats)
+            inb("pv P first", tp[tp < TC], gsm * TC)
+        inb("pv Vs", gsm * TC + cce * (TC + 4) + te, lds_floats)
         n32 = (nt + 31) >> 5
         last = 4 * (8 * (n32 - 1) + 7) + 3
-        chain = tid[tid < group * CW]
-        inb("pv chain P", (chain // CW) * TC + last, group * TC)
-        inb("pv chain Vs", group * TC + (chain % CW) * (TC + 4) + last, lds_floats)
-    ch = tid[tid < group * CW]
+        chain = tid[tid < gs * CW]
+        inb("pv chain P", (chain // CW) * TC + last, gsm * TC)
+        inb("pv chain Vs", gsm * TC + (chain % CW) * (TC + 4) + last, lds_floats)
+    ch = tid[tid < gs * CW]
     col = ch % CW
     ok = (i0[:, None] + col[None, :]) < hd
-    outi = (kvh[:, None, None] * group + (ch // CW)[None, None, :]) * hd + i0[None, :, None] + col[None, None, :]
+    outi = (hb[:, None, None] + (ch // CW)[None, None, :]) * hd + i0[None, :, None] + col[None, None, :]
     inb("pv out", outi[np.broadcast_to(ok[None], outi.shape)], ext.out)
 
 
@@ -306,7 +321,6 @@ def fused(nh, nkv, hd, S, n, ext, TC=AF_TC, cw=CW):
 def pv(nh, nkv, hd, S, pos, ext):
     """qmh_launch_attn_pv's choice of kernel and dynamic LDS bytes."""
     group = nh // nkv
-    assert group <= 16 and group * CW <= WG
     n = pos + 1
     if hd % 4 == 0 and (group == 1 or S <= PV_LONG):
         lds_floats = max(640 + CW * (640 + 4), PV_LONG + 2 * CW * (128 + 4))
@@ -320,7 +334,7 @@ def pv(nh, nkv, hd, S, pos, ext):
             pv_chunks(640, True, nh, nh, hd, S, n, ext, lds_floats)
         return
     TC, MHA = (640, True) if group == 1 else (640, False) if group <= 8 else (256, False)
-    lds_floats = group * TC + CW * (TC + 4)
+    lds_floats = min(group, 16) * TC + CW * (TC + 4)
     assert 4 * lds_floats <= LDS_MAX
     pv_chunks(TC, MHA, nh, nkv, hd, S, n, ext, lds_floats)
 

@@ -195,6 +195,12 @@ def test_fused_attention_stage_timer(gpu, oracle, af_models):
         m.prefill(prompt, 0)  # the timer wrote the caches at its positions
         ids = m.greedy(int(want_ids[0]), len(prompt), 4)
     assert list(ids) == list(want_ids[1:])
+    # past the one-launch kernel's instances the stage timer refuses the one-launch stage
+    with gpu.Model.load(af_models[("af64x", "q8_0")]) as m:
+        with pytest.raises(gpu.QmhError, match="no one-launch attention"):
+            m.time_stage("attn", 3, pos=1030)
+        ms, _ = m.time_stage("attn", 3, pos=1000)
+        assert ms > 0
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])

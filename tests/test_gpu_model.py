@@ -247,6 +247,10 @@ def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
     # two-launch path past 1024 positions
     ("gqa64", dict(dim=256, hidden_dim=320, n_layers=1, n_heads=4, n_kv_heads=1, vocab_size=300, max_seq=1100),
      "q8_0", [(636, 646), (1019, 1029)]),
+    # 32 query heads on one kv head of 64 dims: the 8-column one-launch kernel on a full grid (32 heads
+    # x 8 column groups = 256 workgroups), every head reading the one kv head's K and V
+    ("gqa32x64", dict(dim=2048, hidden_dim=256, n_layers=1, n_heads=32, n_kv_heads=1, vocab_size=300,
+                      max_seq=1040), "q4_0", [(636, 646), (1019, 1029)]),
     # grouped heads (2 and 8 query heads per kv head), head_dim 32 and 16: the per-query-head P.V
     # kernel reading its kv head's V, whole-context and streamed past 640 positions
     ("gqa32", dict(dim=128, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=1300),
@@ -263,6 +267,10 @@ def test_batched_prefill_rows_not_multiple_of_4(gpu, tmp_path, wt):
      "q8_0", [(250, 262), (636, 646)]),
     ("gqa10", dict(dim=40, hidden_dim=96, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=300, max_seq=700),
      "q4_0", [(250, 262), (636, 646)]),
+    # 20 query heads on one kv head of 10 dims: k_attn_pv<256, false> in two sub-groups (16 + 4 heads
+    # per workgroup) around its 256-position chunk boundary
+    ("gqa20x10", dict(dim=200, hidden_dim=128, n_layers=1, n_heads=20, n_kv_heads=1, vocab_size=300, max_seq=300),
+     "q8_0", [(250, 262)]),
     # 12 query heads on one kv head of 10 dims: the 256-position chunks (k_attn_pv<256, false>)
     ("gqa10x12", dict(dim=120, hidden_dim=128, n_layers=1, n_heads=12, n_kv_heads=1, vocab_size=300, max_seq=530),
      "q8_0", [(250, 262), (508, 516)]),
