@@ -69,6 +69,7 @@ int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int want);
 int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream);
 /* longest row the quantized matvec takes, with (norm = 1) or without the RMSNorm prologue */
 int qmh_matvec_max_cols(int norm);
+int qmh_matvec_max_image_cols(void);
 /* f32 weights: plain rows, serial dot per row (src/kernels_scalar.c:6-10) */
 int qmh_launch_matvec_f32(const qmh_mv_args *a, void *stream);
 

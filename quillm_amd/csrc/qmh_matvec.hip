@@ -349,10 +349,16 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
 // activation modes of k_matvec: quantize x (optionally RMSNorm'd first), or copy a quantized
 // image another kernel wrote (QMH_XQ_IMAGE_BYTES layout)
 enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
-// uint4 per thread for an image of up to 16 KiB (nb <= 409)
-template <int NT>
+// uint4 per thread for an image of up to CAP bytes: 16 KiB (nb <= 409) in the instance every
+// matvec of the 7B shapes shares, 24 KiB (nb <= 614: hidden_dim <= 19648, the W2 input of the
+// 13B / Mistral-7B / Llama-3-8B feed-forward widths 13824 and 14336) in a second instance that
+// only rows past 16 KiB of image launch (a third register set in the shared instance cost its W2
+// 1%, measured)
+#define QMH_MV_IMAGE_CAP 16384
+#define QMH_MV_IMAGE_CAP_WIDE 24576
+template <int NT, int CAP = QMH_MV_IMAGE_CAP>
 struct ImageRegs {
-    static constexpr int N = (16384 + 16 * NT - 1) / (16 * NT);
+    static constexpr int N = (CAP + 16 * NT - 1) / (16 * NT);
 };
 
 #ifndef QMH_MV_D
@@ -421,7 +427,7 @@ typedef unsigned int mv_u32x4 __attribute__((ext_vector_type(4)));
 // mode are uniform runtime values): the decode step's kernels then share one copy of this code in
 // the instruction cache, instead of refetching a different instance's code (from HBM, the
 // weight stream having evicted it from L2) at every launch.
-template <int WT, int D, int CHQ4, int NT>
+template <int WT, int D, int CHQ4, int NT, int ICAP = QMH_MV_IMAGE_CAP>
 __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     constexpr int CB = WT == QMH_Q4 ? 16 : 32;           // code bytes per block
     constexpr int NV = CB / 16;                          // uint4 per block
@@ -445,12 +451,12 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
 
     // 1. activation (or image) loads, issued first so waiting for them never waits for weights
     float4 xr[2 * PX], wr[2 * ActRegs<true, NT>::P];
-    uint4 im[ImageRegs<NT>::N];
+    uint4 im[ImageRegs<NT, ICAP>::N];
     const int nimg = (int)(QMH_XQ_IMAGE_BYTES(nb) / 16);
     if (am == MV_ACT_IMAGE) {
         const uint4 *src = (const uint4 *)a.xq_in;
 #pragma unroll
-        for (int k = 0; k < ImageRegs<NT>::N; k++)
+        for (int k = 0; k < ImageRegs<NT, ICAP>::N; k++)
             if (k * NT < nimg) {
                 const int i = k * NT + tid;
                 im[k] = src[i < nimg ? i : nimg - 1];
@@ -493,7 +499,7 @@ __global__ __launch_bounds__(NT) void k_matvec(qmh_mv_args a) {
     if (am == MV_ACT_IMAGE) {
         // global image: codes [nb][32], then d [nb], then code sums [nb] (QMH_XQ_IMAGE_BYTES)
 #pragma unroll
-        for (int k = 0; k < ImageRegs<NT>::N; k++) {
+        for (int k = 0; k < ImageRegs<NT, ICAP>::N; k++) {
             const int i = k * NT + tid;
             if (k * NT < nimg && i < nimg) {
                 const int o = 16 * i;
@@ -772,6 +778,11 @@ extern "C" int qmh_matvec_max_cols(int norm) {
     return (norm ? ActRegs<true, QMH_MV_NT>::P : ActRegs<false, QMH_MV_NT>::P) * QMH_MV_NT * 8;
 }
 
+// the longest row whose input comes as a quantized image (QMH_XQ_IMAGE_BYTES(nb) <= the image registers)
+extern "C" int qmh_matvec_max_image_cols(void) {
+    return (ImageRegs<QMH_MV_NT, QMH_MV_IMAGE_CAP_WIDE>::N * QMH_MV_NT * 16) / 40 * 32;
+}
+
 // Workgroups for k_matvec: `want` (about one per CU; more for matrices of many tiles), never
 // more than ntiles, and enough that a workgroup's records and terms fit the 64 KiB of LDS one
 // workgroup may take. -1: one tile does not fit.
@@ -790,7 +801,8 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     const bool norm = a->norm_w != NULL, image = a->xq_in != NULL;
     if (a->tile_r != 8 && a->tile_r != 16 && a->tile_r != 32 && a->tile_r != 64) return (int)hipErrorInvalidValue;
     if (a->epi == QMH_EPI_SWIGLU && a->tile_r < 32) return (int)hipErrorInvalidValue;  // interleaved W1|W3 tiles
-    if (grid < 1 || grid > a->ntiles || a->cols < 1 || a->cols > qmh_matvec_max_cols(norm) || (norm && image) ||
+    // an image input is bounded by the image registers (checked below), a float input by ActRegs
+    if (grid < 1 || grid > a->ntiles || a->cols < 1 || (!image && a->cols > qmh_matvec_max_cols(norm)) || (norm && image) ||
         (unsigned long long)grid * (unsigned long long)a->ntiles >= (1ull << 32))  // mv_tile0's 32-bit product
         return (int)hipErrorInvalidValue;
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
@@ -798,10 +810,18 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     const size_t lds = mv_lds_bytes(a->nb, a->tile_r, tmax, QMH_MV_CH, a->dtype == QMH_Q4, QMH_MV_NT);
     if (lds > 65536 || (long long)tmax * a->tile_r * a->nb * (a->dtype == QMH_Q4 ? 16 : 32) >= (1ll << 31))
         return (int)hipErrorInvalidValue;
-    if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT>::N * QMH_MV_NT * 16) return (int)hipErrorInvalidValue;
+    if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT, QMH_MV_IMAGE_CAP_WIDE>::N * QMH_MV_NT * 16)
+        return (int)hipErrorInvalidValue;
+    const bool wide = image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT>::N * QMH_MV_NT * 16;
     if ((a->epi == QMH_EPI_SWIGLU_Q) != (a->tile_r == 64)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    if (a->dtype == QMH_Q4)
+    if (wide && a->dtype == QMH_Q4)
+        hipLaunchKernelGGL((k_matvec<QMH_Q4, QMH_MV_D, QMH_MV_CH, QMH_MV_NT, QMH_MV_IMAGE_CAP_WIDE>), dim3(grid),
+                           dim3(QMH_MV_NT), lds, s, *a);
+    else if (wide)
+        hipLaunchKernelGGL((k_matvec<QMH_Q8, QMH_MV_D, QMH_MV_CH, QMH_MV_NT, QMH_MV_IMAGE_CAP_WIDE>), dim3(grid),
+                           dim3(QMH_MV_NT), lds, s, *a);
+    else if (a->dtype == QMH_Q4)
         hipLaunchKernelGGL((k_matvec<QMH_Q4, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a);
     else
         hipLaunchKernelGGL((k_matvec<QMH_Q8, QMH_MV_D, QMH_MV_CH, QMH_MV_NT>), dim3(grid), dim3(QMH_MV_NT), lds, s, *a);

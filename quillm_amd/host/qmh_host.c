@@ -779,13 +779,19 @@ static int model_build(qmh_model *m, const qmh_tensor_view *tok_embd, const qmh_
             return fail("layer %d: wq/wk/wv must share one dtype", l);
         if (t[6].dtype != t[8].dtype) return fail("layer %d: w1/w3 must share one dtype", l);
     }
-    /* LDS budget of the kernels (64 KiB per workgroup) */
+    /* LDS budget of the kernels (64 KiB per workgroup); W2's input is the quantized image W1|W3 writes
+     * when both are quantized (every layer), else hb quantized in W2's prologue */
+    int h_image = 1;
+    for (int l = 0; l < c->n_layers; l++)
+        if (layers[9 * l + 6].dtype == QMH_F32 || layers[9 * l + 7].dtype == QMH_F32) h_image = 0;
+    const int hmax = h_image && qmh_matvec_max_image_cols() > qmh_matvec_max_cols(0) ? qmh_matvec_max_image_cols()
+                                                                                      : qmh_matvec_max_cols(0);
     const int nbD = (int)((D + 31) / 32), nbH = (int)((H + 31) / 32);
     if (qmh_matvec_grid(1, nbD, 64, QMH_Q4_0, 1) < 1 || qmh_matvec_grid(1, nbD, QMH_TILE_R, QMH_Q4_0, 1) < 1 ||
         qmh_matvec_grid(1, nbD, 8, QMH_Q4_0, 1) < 1 || qmh_matvec_grid(1, nbH, 8, QMH_Q4_0, 1) < 1 ||
-        D > qmh_matvec_max_cols(1) || H > qmh_matvec_max_cols(0))
+        D > qmh_matvec_max_cols(1) || H > hmax)
         return fail("model dims exceed the kernels' limits (dim <= %d, hidden_dim <= %d)", qmh_matvec_max_cols(1),
-                    qmh_matvec_max_cols(0));
+                    hmax);
     /* any group (the reference's only rule is n_heads % n_kv_heads == 0): the kv-head P.V kernel takes
      * it in sub-groups of up to 16 query heads */
     const int64_t gsub = m->group < 16 ? m->group : 16;

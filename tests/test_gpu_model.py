@@ -298,3 +298,40 @@ def test_long_context_decode_matches_oracle(gpu, oracle, tmp_path, name, dims, w
                 got = m.forward(int(toks[i]), i)
                 assert np.array_equal(bits(got), bits(want[i])), f"position {i}: max |d| {np.abs(got - want[i]).max()}"
             p = hi
+
+
+@pytest.mark.parametrize("hidden,wt", [(14336, "q4_0"), (13824, "q8_0")])
+def test_wide_hidden_matches_oracle(gpu, oracle, tmp_path, hidden, wt):
+    """Feed-forward widths past 12288 (Llama-2-13B's 13824, Mistral-7B's and Llama-3-8B's 14336): W2's
+    input arrives as W1|W3's quantized image of 432-448 blocks. Prefill logits, decode forwards and the
+    device greedy loop bitwise the oracle's; batched forwards (multi-token matvec at 2 sequences, skinny
+    matmul at 5) bitwise the oracle's single-sequence logits."""
+    cfg = gpu.QmhConfig(dim=512, hidden_dim=hidden, n_layers=2, n_heads=8, n_kv_heads=2, vocab_size=300,
+                        max_seq=80, rope_theta=10000.0, norm_eps=1e-5)
+    path = str(tmp_path / f"wide_h{hidden}_{wt}.qlm")
+    gpu.gen_model(path, cfg, wt, seed=23, threads=4)
+    P, G = 40, 8
+    prompt = gpu.prompt_ids(P, 300, seed=19)
+    say(f"case hidden {hidden}/{wt}: oracle {P}+{G}")
+    want, want_ids = oracle.run_model(path, prompt, n_gen=G)
+    with gpu.Model.load(path) as m:
+        lg = m.prefill(prompt, 0, want_logits=True)
+        assert np.array_equal(bits(lg), bits(want[:P])), "prefill logits"
+        tok = int(want_ids[0])
+        for g in range(G):
+            got = m.forward(tok, P + g)
+            assert np.array_equal(bits(got), bits(want[P + g])), f"position {P + g}"
+            tok = int(np.argmax(got))
+        m.prefill(prompt, 0)
+        ids = m.greedy(int(want_ids[0]), P, G)
+        assert list(ids) == list(want_ids[1:])
+        rs = np.random.default_rng(hidden)
+        for B in (2, 5):
+            toks = [rs.integers(0, 300, 6 + i).astype(np.int32) for i in range(B)]
+            wl = [oracle.run_model(path, t, 0)[0] for t in toks]
+            with gpu.Batch(m, B) as bt:
+                for k in range(6 + B - 1):
+                    pos = [min(k, 6 + i - 1) for i in range(B)]
+                    out = bt.forward([int(toks[i][pos[i]]) for i in range(B)], pos)
+                    for i in range(B):
+                        assert np.array_equal(bits(out[i]), bits(wl[i][pos[i]])), f"B={B} step {k} sequence {i}"
