@@ -350,12 +350,12 @@ __device__ __forceinline__ void mv_epilogue(const qmh_mv_args &a, int row, float
 // image another kernel wrote (QMH_XQ_IMAGE_BYTES layout)
 enum { MV_ACT = 0, MV_ACT_NORM = 1, MV_ACT_IMAGE = 2 };
 // uint4 per thread for an image of up to CAP bytes: 16 KiB (nb <= 409) in the instance every
-// matvec of the 7B shapes shares, 24 KiB (nb <= 614: hidden_dim <= 19648, the W2 input of the
-// 13B / Mistral-7B / Llama-3-8B feed-forward widths 13824 and 14336) in a second instance that
-// only rows past 16 KiB of image launch (a third register set in the shared instance cost its W2
-// 1%, measured)
+// matvec of the 7B shapes shares, 40 KiB (nb <= 1024: hidden_dim <= 32768, the W2 input of the
+// 13B / Mistral-7B / Llama-3-8B / 70B feed-forward widths 13824, 14336 and 28672) in a second
+// instance that only rows past 16 KiB of image launch (a third register set in the shared instance
+// cost its W2 1%, measured)
 #define QMH_MV_IMAGE_CAP 16384
-#define QMH_MV_IMAGE_CAP_WIDE 24576
+#define QMH_MV_IMAGE_CAP_WIDE 40960
 template <int NT, int CAP = QMH_MV_IMAGE_CAP>
 struct ImageRegs {
     static constexpr int N = (CAP + 16 * NT - 1) / (16 * NT);
@@ -786,12 +786,18 @@ extern "C" int qmh_matvec_max_image_cols(void) {
 // Workgroups for k_matvec: `want` (about one per CU; more for matrices of many tiles), never
 // more than ntiles, and enough that a workgroup's records and terms fit the 64 KiB of LDS one
 // workgroup may take. -1: one tile does not fit.
+// LDS budgets of a k_matvec workgroup: 64 KiB, or where one tile's records and terms do not fit
+// that (rows of more than ~7000 columns in 64-row tiles, W2's input past ~13000), up to 152 KiB
+// (one workgroup per CU either way; the 7B shapes' grids are those of the 64 KiB budget)
+#define MV_LDS 65536
+#define MV_LDS_WIDE (152 * 1024)
 extern "C" int qmh_matvec_grid(int ntiles, int nb, int tile_r, int dtype, int want) {
     if (ntiles < 1 || nb < 1 || (dtype != QMH_Q4 && dtype != QMH_Q8)) return -1;
     const size_t rec = (size_t)mv_nrec(nb, tile_r, QMH_MV_CH, dtype == QMH_Q4, QMH_MV_NT) * MV_REC;
     const size_t per = 4 * (size_t)tile_r * mv_term_stride(nb);
-    if (rec + per > 65536) return -1;
-    const int maxt = (int)((65536 - rec) / per);
+    const size_t budget = rec + per <= MV_LDS ? MV_LDS : MV_LDS_WIDE;
+    if (rec + per > budget) return -1;
+    const int maxt = (int)((budget - rec) / per);
     int g = want < ntiles ? want : ntiles;
     const int need = (ntiles + maxt - 1) / maxt;
     return g > need ? g : need;
@@ -808,7 +814,7 @@ extern "C" int qmh_launch_matvec(const qmh_mv_args *a, int grid, void *stream) {
     if (a->dtype != QMH_Q4 && a->dtype != QMH_Q8) return (int)hipErrorInvalidValue;
     const int tmax = (a->ntiles + grid - 1) / grid;
     const size_t lds = mv_lds_bytes(a->nb, a->tile_r, tmax, QMH_MV_CH, a->dtype == QMH_Q4, QMH_MV_NT);
-    if (lds > 65536 || (long long)tmax * a->tile_r * a->nb * (a->dtype == QMH_Q4 ? 16 : 32) >= (1ll << 31))
+    if (lds > MV_LDS_WIDE || (long long)tmax * a->tile_r * a->nb * (a->dtype == QMH_Q4 ? 16 : 32) >= (1ll << 31))
         return (int)hipErrorInvalidValue;
     if (image && QMH_XQ_IMAGE_BYTES(a->nb) > (size_t)ImageRegs<QMH_MV_NT, QMH_MV_IMAGE_CAP_WIDE>::N * QMH_MV_NT * 16)
         return (int)hipErrorInvalidValue;
