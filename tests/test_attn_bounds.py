@@ -6,23 +6,24 @@ the test models) and positions on both sides of each chunk boundary, and checked
 extent of its buffer: the per-layer caches K [kvd][max_seq] and V [max_seq][kvd], the scores
 att [n_heads][max_seq], q and out [n_heads*head_dim], and the dynamic LDS bytes the launcher
 passes. The formulas restate the kernels' own index arithmetic, line by line:
-  * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:24-61 (launcher :63-81)
-  * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:368-400 (launcher :402-416): clamped float4 K
+  * k_attn_scores<HD>     quillm_amd/csrc/qmh_attn.hip:25-68 (launcher :70-88)
+  * k_attn_scores_t<HD>   quillm_amd/csrc/qmh_ops.hip:431-464 (launcher :467-480): clamped float4 K
                           loads past the last position (t <= max_seq-4)
-  * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:92-246 (k_attn_pv :249-255): unconditional V
+  * attn_pv_chunks<TC,M>  quillm_amd/csrc/qmh_attn.hip:100-257 (k_attn_pv :259-266): unconditional V
                           and score loads clamped to position n-1 / score 0, columns to head_dim-1
-  * pv_mha_long<LA>       quillm_amd/csrc/qmh_attn.hip:262-380: exponentials of up to 8192 positions,
+  * pv_mha_long<LA>       quillm_amd/csrc/qmh_attn.hip:274-379: exponentials of up to 8192 positions,
                           V pieces of 128 positions loaded LA pieces ahead (clamped to the last piece
                           and position n-1), two staged buffers
-  * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:393-530: one workgroup per query head, float4 V
+  * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:502-553: one workgroup per query head, float4 V
                           loads of its kv head clamped to position n-1 and column head_dim-4
-  * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:532-555: kernel choice and dynamic LDS
-  * k_attn_fused<HD,TC,CW> quillm_amd/csrc/qmh_attn.hip (the one-launch attention for n <= TC, TC 640
-                          for head_dim 48/64/128 and 1024 for head_dim 64/128 (48 too at CW 8), CW =
-                          16 or 8 output columns per workgroup): the K slice of each workgroup (clamped float4s), its LDS rows, the epoch-tagged
-                          score words, and that the slices of a head's workgroups cover its n
-                          positions exactly once (a position nobody writes would leave its readers
-                          waiting until their bounded wait runs out)
+  * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:900-924: kernel choice and dynamic LDS
+  * k_attn_fused<HD,TC,CW> quillm_amd/csrc/qmh_attn.hip:682-813, its V sum pv_short_flow :561-640 (the
+                          one-launch attention for n <= TC, TC 640 for head_dim 48/64/128 and 1024
+                          for head_dim 64/128 (48 too at CW 8), CW = 16 or 8 output columns per
+                          workgroup): the K slice of each workgroup (clamped float4s), its LDS rows,
+                          the epoch-tagged score words, and that the slices of a head's workgroups
+                          cover its n positions exactly once (a position nobody writes would leave
+                          its readers waiting until their bounded wait runs out)
 This is a model: a kernel edit that changes an index must change it here too.
 """
 import numpy as np
