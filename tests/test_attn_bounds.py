@@ -17,7 +17,7 @@ passes. The formulas restate the kernels' own index arithmetic, line by line:
   * k_attn_pv_mha<640>    quillm_amd/csrc/qmh_attn.hip:502-553: one workgroup per query head, float4 V
                           loads of its kv head clamped to position n-1 and column head_dim-4
   * qmh_launch_attn_pv    quillm_amd/csrc/qmh_attn.hip:900-924: kernel choice and dynamic LDS
-  * k_attn_fused<HD,TC,CW> quillm_amd/csrc/qmh_attn.hip:682-813, its V sum pv_short_flow :561-640 (the
+  * k_attn_fused<HD,TC,CW> quillm_amd/csrc/qmh_attn.hip:682-813, its V sum pv_short_flow :561-645 (the
                           one-launch attention for n <= TC, TC 640 for head_dim 48/64/128 and 1024
                           for head_dim 64/128 (48 too at CW 8), CW = 16 or 8 output columns per
                           workgroup): the K slice of each workgroup (clamped float4s), its LDS rows,
