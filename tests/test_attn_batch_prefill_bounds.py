@@ -7,7 +7,7 @@ positions, and checked against its buffer's extent:
   * qmh_launch_bt_attention  quillm_amd/csrc/qmh_batch.hip:222-248: the kernel choice by B, shape
                              and the largest position
   * k_attn_scores<HD> and k_attn_pv_mha<640> over blockIdx.z (qmh_launch_attn_batch,
-                             quillm_amd/csrc/qmh_attn.hip:906-926): sequence z at q + z*n_heads*hd,
+                             quillm_amd/csrc/qmh_attn.hip:930-950): sequence z at q + z*n_heads*hd,
                              caches at + z*kv_stride, scores at + z*n_heads*max_seq, position pos[z]
   * k_bt_scores / k_bt_softmax / k_bt_pv  quillm_amd/csrc/qmh_batch.hip:16-117
   * k_bt_attn                quillm_amd/csrc/qmh_batch.hip:129-219 (V chunks of 128 positions
