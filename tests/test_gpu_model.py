@@ -300,21 +300,22 @@ def test_long_context_decode_matches_oracle(gpu, oracle, tmp_path, name, dims, w
             p = hi
 
 
-@pytest.mark.parametrize("dim,hidden,heads,kv,layers,wt", [
-    (512, 14336, 8, 2, 2, "q4_0"), (512, 13824, 8, 2, 2, "q8_0"), (512, 28672, 8, 2, 1, "q4_0"),
-    (8192, 512, 64, 8, 1, "q8_0")])
-def test_wide_hidden_matches_oracle(gpu, oracle, tmp_path, dim, hidden, heads, kv, layers, wt):
+@pytest.mark.parametrize("dim,hidden,heads,kv,layers,wt,P", [
+    (512, 14336, 8, 2, 2, "q4_0", 40), (512, 13824, 8, 2, 2, "q8_0", 40), (512, 28672, 8, 2, 1, "q4_0", 100),
+    (8192, 512, 64, 8, 1, "q8_0", 40)])
+def test_wide_hidden_matches_oracle(gpu, oracle, tmp_path, dim, hidden, heads, kv, layers, wt, P):
     """Feed-forward widths past 12288 (Llama-2-13B's 13824, Mistral-7B's and Llama-3-8B's 14336, the 70B
     shapes' 28672): W2's input arrives as W1|W3's quantized image of 432-896 blocks (a second matvec
     instance past 16 KiB of image); and the 70B width 8192 with 64 query heads on 8 kv heads, whose
     64-row W1|W3 tiles need more than 64 KiB of LDS per workgroup. Prefill logits, decode forwards and
     the device greedy loop bitwise the oracle's; batched forwards (multi-token matvec at 2 sequences,
-    skinny matmul at 5) bitwise the oracle's single-sequence logits."""
+    skinny matmul at 5) bitwise the oracle's single-sequence logits. A 100-token prompt runs the tiled
+    prefill matmul, whose W1|W3 epilogue writes W2's image."""
     cfg = gpu.QmhConfig(dim=dim, hidden_dim=hidden, n_layers=layers, n_heads=heads, n_kv_heads=kv,
-                        vocab_size=300, max_seq=80, rope_theta=10000.0, norm_eps=1e-5)
+                        vocab_size=300, max_seq=P + 40, rope_theta=10000.0, norm_eps=1e-5)
     path = str(tmp_path / f"wide_d{dim}_h{hidden}_{wt}.qlm")
     gpu.gen_model(path, cfg, wt, seed=23, threads=4)
-    P, G = 40, 8
+    G = 8
     prompt = gpu.prompt_ids(P, 300, seed=19)
     say(f"case dim {dim} hidden {hidden}/{wt}: oracle {P}+{G}")
     want, want_ids = oracle.run_model(path, prompt, n_gen=G)
