@@ -1,6 +1,7 @@
 """Whole-model parity of the device forward with the CPU oracle and with the compiled
 reference (scalar ISA), through the C ABI: per-position logits bit-exact, greedy ids identical,
 prefill == sequential forwards, bad inputs rejected, bitwise run-to-run determinism."""
+import os
 import sys
 
 import numpy as np
@@ -340,3 +341,34 @@ def test_wide_hidden_matches_oracle(gpu, oracle, tmp_path, dim, hidden, heads, k
                     out = bt.forward([int(toks[i][pos[i]]) for i in range(B)], pos)
                     for i in range(B):
                         assert np.array_equal(bits(out[i]), bits(wl[i][pos[i]])), f"B={B} step {k} sequence {i}"
+
+
+@pytest.mark.parametrize("name,dim,hidden,layers,heads,kv,vocab,theta", [
+    ("llama3_8b", 4096, 14336, 32, 32, 8, 128256, 500000.0), ("llama2_13b", 5120, 13824, 40, 40, 40, 32000, 10000.0)])
+def test_full_size_shapes_vs_reference(gpu, tmp_path, name, dim, hidden, layers, heads, kv, vocab, theta):
+    """Full-size Llama-3-8B and Llama-2-13B shapes in Q4_0 (every layer and the real vocabulary; random
+    weights): the batched prefill's 8 prompt logits and 8 greedy forwards bitwise the compiled reference's
+    scalar ISA, and the device greedy loop's ids the reference's."""
+    cfg = gpu.QmhConfig(dim, hidden, layers, heads, kv, vocab, 64, theta, 1e-5)
+    path = str(tmp_path / f"{name}.qlm")
+    say(f"case {name}: generate")
+    gpu.gen_model(path, cfg, "q4_0", seed=1, threads=16)
+    try:
+        P, G = 8, 8
+        prompt = gpu.prompt_ids(P, vocab, seed=1234)
+        say(f"case {name}: reference, {P} prompt + {G} greedy")
+        res, rl = ref_run(path, prompt, G, isa="scalar", threads=16)
+        rl = rl.reshape(P + G, vocab)
+        toks = res["tokens"]
+        with gpu.Model.load(path) as m:
+            say(f"case {name}: device prefill and forwards")
+            lg = m.prefill(prompt, 0, want_logits=True)
+            assert np.array_equal(bits(lg), bits(rl[:P])), "prefill logits"
+            for g in range(G):
+                got = m.forward(toks[g], P + g)
+                assert np.array_equal(bits(got), bits(rl[P + g])), f"position {P + g}"
+            say(f"case {name}: device greedy")
+            m.prefill(prompt, 0)
+            assert list(m.greedy(toks[0], P, G)) == toks[1:]
+    finally:
+        os.remove(path)
